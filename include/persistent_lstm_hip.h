@@ -1,0 +1,115 @@
+/*
+ * persistent_lstm_hip.h -- C ABI of the MI355X (gfx950) stacked LSTM + Linear inference forward.
+ *
+ * Library: persistent_lstm_hip_amd/lib/libpersistent_lstm_hip.so
+ *
+ * Conventions
+ *   - Every pointer named *_dev, and every tensor argument, is device memory on the current HIP
+ *     device.  fp16 tensors are IEEE binary16 (torch.float16), row-major, contiguous.
+ *   - `stream` is a hipStream_t (may be NULL for the null stream).  Entry points only enqueue
+ *     work on that stream; none of them synchronises except plh_status().
+ *   - Return value: PLH_OK, or an error code; plh_last_error() gives the calling thread's message.
+ *     PLH_ERR_INVALID and PLH_ERR_UNSUPPORTED correspond to the reference's std::invalid_argument
+ *     (Python ValueError, persistent_lstm_op.cpp:7-11); PLH_ERR_HIP to its std::runtime_error with
+ *     the hipGetErrorString text (Python RuntimeError, persistent_lstm_hip.cu:1730-1735).
+ *   - Model geometry: I = input size, H = hidden size, L = layers, O = Linear output size
+ *     (O = 0: no head).  Gate order along the 4H axis is i, f, g, o as in torch.nn.LSTM.
+ *   - Numerics: fp16 weights and activations, fp32 MFMA accumulation, c kept in fp32, h rounded
+ *     to fp16 every step, fused bias b_ih + b_hh summed in fp32, head accumulated in fp32 and
+ *     written as fp16.
+ *
+ * Reference interface each entry point replaces (mantuoluozk/persistent_lstm_hip):
+ *   bindings.cpp:154-165 exports the pybind functions the Python dispatcher calls.  The weight
+ *   repacking that model.py:542-582 / :20-27 does on the Python side becomes plh_pack_regressor,
+ *   and the family of fixed-shape forwards collapses into plh_forward.
+ */
+#ifndef PERSISTENT_LSTM_HIP_H
+#define PERSISTENT_LSTM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PLH_OK 0
+#define PLH_ERR_INVALID 1     /* bad argument (shape, size, null pointer)        -> ValueError   */
+#define PLH_ERR_UNSUPPORTED 2 /* geometry outside what the kernels implement      -> ValueError   */
+#define PLH_ERR_HIP 3         /* HIP runtime error                                -> RuntimeError */
+#define PLH_ERR_DEVICE 4      /* the persistent kernel reported a failure status  -> RuntimeError */
+
+/* Bits of the device status word read by plh_status(). */
+#define PLH_STATUS_TIMEOUT 1u /* a layer hand-off wait exceeded its time limit; outputs are NaN */
+
+/* ABI version of this header. */
+int plh_abi_version(void);
+
+/* Message describing the last error raised on the calling thread ("" if none). */
+const char* plh_last_error(void);
+
+/* 1 if plh_forward implements this geometry, else 0 (plh_last_error() says why).
+ * Replaces the shape predicates PersistentLSTMRegressor._can_use_specialized_regressor_hip
+ * (model.py:432-441) and NativeModuleFallback._can_use_generic_projected_module (model.py:131-165). */
+int plh_supports(int input_size, int hidden_size, int num_layers, int output_size);
+
+/* Bytes of the packed-weight blob for a geometry (negative on invalid geometry). */
+int64_t plh_packed_bytes(int input_size, int hidden_size, int num_layers, int output_size);
+
+/*
+ * Pack torch-layout fp16 parameters into the kernel's resident-weight layout.
+ *   w_ih[l]: weight_ih_l{l} [4H, l == 0 ? I : H]      w_hh[l]: weight_hh_l{l} [4H, H]
+ *   b_ih[l], b_hh[l]: [4H] (b_hh[l] or the whole b_hh array may be NULL: treated as zero, which also
+ *                     lets a caller pass the reference's pre-fused bias b_ih + b_hh in b_ih)
+ *   lin_w [O, H], lin_b [O] (ignored when O == 0)
+ * w_ih, w_hh, b_ih, b_hh are HOST arrays of L device pointers.
+ * Replaces the repack cache fill of model.py:542-582 (kpairs packing, model.py:20-27) and the
+ * per-call weight handling of persistent_lstm_regressor_forward_generic_projected_hip
+ * (persistent_lstm_hip.cu:2923-3000).
+ */
+int plh_pack_regressor(int input_size, int hidden_size, int num_layers, int output_size,
+                       const void* const* w_ih, const void* const* w_hh, const void* const* b_ih,
+                       const void* const* b_hh, const void* lin_w, const void* lin_b,
+                       void* packed_dev, int64_t packed_bytes, void* stream);
+
+/* Bytes of device workspace plh_forward needs for (geometry, batch, seq_len). */
+int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int output_size, int batch,
+                            int seq_len);
+
+/*
+ * Stacked LSTM (+ optional Linear head) forward over x [batch, seq_len, I] fp16 (batch_first).
+ *   lengths   device int32 [batch] or NULL.  NULL: every row runs seq_len steps.  Otherwise
+ *             packed-sequence semantics: row b runs lengths[b] steps, its state is frozen after,
+ *             out_seq is zero past its length and the head reads its state at its last step.
+ *   h0, c0    device fp16 [L, batch, H] initial state, or NULL for zeros (nn.LSTM hx).
+ *   out       device fp16 [batch, O]: Linear(h_n[L-1]) (= Linear(out_seq[:, -1]) for full rows).
+ *   out_seq   device fp16 [batch, seq_len, H]: last layer's outputs, or NULL.
+ *   h_n, c_n  device fp16 [L, batch, H] final states, or NULL.
+ *   probe_steps device int32 [n_probe], strictly increasing step counts in [1, seq_len];
+ *             probe_h / probe_c device fp32 [n_probe, L, batch, H] receive every layer's state
+ *             after that many steps (h as rounded to fp16, c in fp32).  n_probe = 0: no probes.
+ *   workspace device memory of at least plh_workspace_bytes(...) bytes, 256-byte aligned.
+ * Any output pointer may be NULL.  Asynchronous on `stream`.
+ * Replaces persistent_lstm4_forward_interleaved (bindings.cpp:157, persistent_lstm_hip.cu:2126-2254)
+ * and persistent_lstm_regressor_forward_generic_projected (bindings.cpp:163,
+ * persistent_lstm_hip.cu:2923-3181), whose signatures return only the [batch, O] head output;
+ * the state/sequence/probe outputs serve the nn.LSTM drop-in (model.py:323-395) and drift checks.
+ */
+int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num_layers, int output_size,
+                const void* x, int batch, int seq_len, const int32_t* lengths, const void* h0,
+                const void* c0, void* out, void* out_seq, void* h_n, void* c_n,
+                const int32_t* probe_steps, int n_probe, float* probe_h, float* probe_c, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
+/* Synchronise `stream` and read the status word the last plh_forward left in `workspace`
+ * (0 = success, else PLH_STATUS_* bits).  Returns PLH_OK or PLH_ERR_HIP. */
+int plh_status(const void* workspace, uint32_t* status, void* stream);
+
+/* out[r, c] = in[0, c] for r < rows (fp16).  Replaces repeat_first_row
+ * (bindings.cpp:164, persistent_lstm_hip.cu:1684-1695, :1784-1809). */
+int plh_repeat_first_row(const void* in, void* out, int rows, int cols, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PERSISTENT_LSTM_HIP_H */

@@ -1,0 +1,242 @@
+// plh_capi.hip -- extern "C" entry points declared in include/persistent_lstm_hip.h.
+//
+// Argument checking follows the reference's boundary (persistent_lstm_op.cpp:7-11 raises
+// std::invalid_argument for bad shapes; persistent_lstm_hip.cu:1730-1735 turns HIP errors into
+// std::runtime_error): here they become PLH_ERR_INVALID / PLH_ERR_HIP plus a message.  Unlike the
+// reference there is no silent fallback: a geometry the kernels do not implement is an error.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "plh_internal.h"
+#include "../../include/persistent_lstm_hip.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int fail_hip(hipError_t e, const char* what) {
+  return fail(PLH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Co-resident workgroup capacity per (device, HP), queried once.
+std::mutex g_cap_mu;
+std::unordered_map<long long, int> g_cap;
+
+int capacity(const plh::Geometry& g, hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return 0;
+  const long long key = (long long)dev * 4096 + g.HP;
+  {
+    std::lock_guard<std::mutex> lk(g_cap_mu);
+    auto it = g_cap.find(key);
+    if (it != g_cap.end()) return it->second;
+  }
+  const int c = plh::recurrent_capacity(g, err);
+  if (*err != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lk(g_cap_mu);
+  g_cap[key] = c;
+  return c;
+}
+
+// Rows per persistent launch: every (layer, tile) workgroup of a launch must be co-resident.
+// Without a device (capacity unknown) the plan assumes one workgroup per CU of a 256-CU MI355X.
+int plan_chunk_rows(const plh::Geometry& g, int batch, int cap) {
+  const int tiles_total = (batch + 15) / 16;
+  int tiles = cap / g.L;
+  if (tiles >= 8) tiles &= ~7;  // keep the XCD-aware mapping available
+  tiles = std::max(1, std::min(tiles, tiles_total));
+  return tiles * 16;
+}
+
+bool geometry(int I, int H, int L, int O, plh::Geometry* g) {
+  std::string why;
+  if (!plh::make_geometry(I, H, L, O, g, &why)) {
+    g_last_error = why;
+    return false;
+  }
+  return true;
+}
+
+int geometry_code(int I, int H, int L, int O) {
+  return (I <= 0 || H <= 0 || L <= 0 || O < 0) ? PLH_ERR_INVALID : PLH_ERR_UNSUPPORTED;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int plh_abi_version(void) { return 1; }
+
+const char* plh_last_error(void) { return g_last_error.c_str(); }
+
+int plh_supports(int input_size, int hidden_size, int num_layers, int output_size) {
+  plh::Geometry g;
+  return geometry(input_size, hidden_size, num_layers, output_size, &g) ? 1 : 0;
+}
+
+int64_t plh_packed_bytes(int input_size, int hidden_size, int num_layers, int output_size) {
+  plh::Geometry g;
+  if (!geometry(input_size, hidden_size, num_layers, output_size, &g)) return -1;
+  return (int64_t)plh::packed_layout(g).total;
+}
+
+int plh_pack_regressor(int input_size, int hidden_size, int num_layers, int output_size,
+                       const void* const* w_ih, const void* const* w_hh, const void* const* b_ih,
+                       const void* const* b_hh, const void* lin_w, const void* lin_b, void* packed_dev,
+                       int64_t packed_bytes, void* stream) {
+  plh::Geometry g;
+  if (!geometry(input_size, hidden_size, num_layers, output_size, &g))
+    return geometry_code(input_size, hidden_size, num_layers, output_size);
+  const plh::PackedLayout p = plh::packed_layout(g);
+  if (!packed_dev || packed_bytes < (int64_t)p.total)
+    return fail(PLH_ERR_INVALID, "packed buffer missing or smaller than plh_packed_bytes()");
+  if (!aligned(packed_dev, 256)) return fail(PLH_ERR_INVALID, "packed buffer must be 256-byte aligned");
+  if (!w_ih || !w_hh || !b_ih) return fail(PLH_ERR_INVALID, "w_ih, w_hh and b_ih arrays are required");
+  if (output_size > 0 && !lin_w) return fail(PLH_ERR_INVALID, "lin_w is required when output_size > 0");
+  hipStream_t s = (hipStream_t)stream;
+  char* base = (char*)packed_dev;
+  for (int l = 0; l < g.L; ++l) {
+    if (!w_ih[l] || !w_hh[l]) return fail(PLH_ERR_INVALID, "null weight pointer for layer " + std::to_string(l));
+    hipError_t e = plh::launch_pack_layer(g, l, (const _Float16*)w_ih[l], (const _Float16*)w_hh[l],
+                                          (_Float16*)(base + p.wpack), s);
+    if (e != hipSuccess) return fail_hip(e, "pack_layer launch");
+    e = plh::launch_pack_bias(g, l, (const _Float16*)b_ih[l], b_hh ? (const _Float16*)b_hh[l] : nullptr,
+                              (float*)(base + p.bias), s);
+    if (e != hipSuccess) return fail_hip(e, "pack_bias launch");
+  }
+  hipError_t e = plh::launch_pack_linear(g, (const _Float16*)lin_w, (const _Float16*)lin_b,
+                                         (float*)(base + p.wlin), (float*)(base + p.blin), s);
+  if (e != hipSuccess) return fail_hip(e, "pack_linear launch");
+  return PLH_OK;
+}
+
+int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int output_size, int batch,
+                            int seq_len) {
+  plh::Geometry g;
+  if (!geometry(input_size, hidden_size, num_layers, output_size, &g)) return -1;
+  if (batch < 0 || seq_len < 0) {
+    g_last_error = "batch and seq_len must be non-negative";
+    return -1;
+  }
+  hipError_t err = hipSuccess;
+  int cap = capacity(g, &err);
+  if (err != hipSuccess || cap <= 0) cap = 256;  // planning without a device: 1 WG per CU, 256 CUs
+  const int rows = plan_chunk_rows(g, std::max(batch, 1), cap);
+  return (int64_t)plh::workspace_layout(g, seq_len, rows).total;
+}
+
+int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num_layers, int output_size,
+                const void* x, int batch, int seq_len, const int32_t* lengths, const void* h0, const void* c0,
+                void* out, void* out_seq, void* h_n, void* c_n, const int32_t* probe_steps, int n_probe,
+                float* probe_h, float* probe_c, void* workspace, int64_t workspace_bytes, void* stream) {
+  plh::Geometry g;
+  if (!geometry(input_size, hidden_size, num_layers, output_size, &g))
+    return geometry_code(input_size, hidden_size, num_layers, output_size);
+  if (batch < 0 || seq_len < 0) return fail(PLH_ERR_INVALID, "batch and seq_len must be non-negative");
+  if (!packed_dev) return fail(PLH_ERR_INVALID, "packed weights are required");
+  if (batch > 0 && seq_len > 0 && !x) return fail(PLH_ERR_INVALID, "x is required");
+  if (n_probe < 0 || (n_probe > 0 && (!probe_steps || !probe_h || !probe_c)))
+    return fail(PLH_ERR_INVALID, "probe_steps, probe_h and probe_c are required when n_probe > 0");
+  if (n_probe > seq_len) return fail(PLH_ERR_INVALID, "more probe steps than sequence steps");
+  if (!workspace || !aligned(workspace, 256)) return fail(PLH_ERR_INVALID, "workspace must be 256-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+
+  hipError_t err = hipSuccess;
+  const int cap = capacity(g, &err);
+  if (err != hipSuccess) return fail_hip(err, "occupancy query");
+  if (cap < g.L)
+    return fail(PLH_ERR_UNSUPPORTED, "the device cannot hold one workgroup per layer co-resident (layers = " +
+                                         std::to_string(g.L) + ", capacity = " + std::to_string(cap) + ")");
+  const int chunk_rows = plan_chunk_rows(g, std::max(batch, 1), cap);
+  const plh::WorkspaceLayout w = plh::workspace_layout(g, seq_len, chunk_rows);
+  if (workspace_bytes < (int64_t)w.total)
+    return fail(PLH_ERR_INVALID, "workspace smaller than plh_workspace_bytes()");
+
+  const plh::PackedLayout p = plh::packed_layout(g);
+  char* ws = (char*)workspace;
+  const char* pk = (const char*)packed_dev;
+  uint32_t* status = (uint32_t*)(ws + w.status);
+  uint32_t* counters = (uint32_t*)(ws + w.counters);
+
+  err = plh::launch_zero_u32(status, 1, s);
+  if (err != hipSuccess) return fail_hip(err, "status reset");
+  if (batch == 0) return PLH_OK;
+
+  plh::ForwardArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = (const _Float16*)x;
+  a.lengths = lengths;
+  a.wpack = (const _Float16*)(pk + p.wpack);
+  a.bias = (const float*)(pk + p.bias);
+  a.wlin = (const float*)(pk + p.wlin);
+  a.blin = (const float*)(pk + p.blin);
+  a.xp = (plh::f16x8_t*)(ws + w.xp);
+  a.hseq = (plh::f16x8_t*)(ws + w.hseq);
+  a.counters = counters;
+  a.status = status;
+  a.h0 = (const _Float16*)h0;
+  a.c0 = (const _Float16*)c0;
+  a.out = output_size > 0 ? (_Float16*)out : nullptr;
+  a.out_seq = (_Float16*)out_seq;
+  a.h_n = (_Float16*)h_n;
+  a.c_n = (_Float16*)c_n;
+  a.probe_steps = probe_steps;
+  a.probe_h = probe_h;
+  a.probe_c = probe_c;
+  a.n_probe = n_probe;
+  a.B = batch;
+  a.T = seq_len;
+  a.I = g.I;
+  a.H = g.H;
+  a.L = g.L;
+  a.O = g.O;
+  a.kc_in0 = g.kc_in0;
+
+  for (int row0 = 0; row0 < batch; row0 += chunk_rows) {
+    const int rows = std::min(chunk_rows, batch - row0);
+    a.row0 = row0;
+    a.row_end = row0 + rows;
+    a.ntile = (rows + 15) / 16;
+    a.rows_pad = a.ntile * 16;
+    a.xcd_map = (a.ntile % 8 == 0) ? 1 : 0;
+    err = plh::launch_zero_u32(counters, (size_t)g.L * a.ntile, s);
+    if (err != hipSuccess) return fail_hip(err, "counter reset");
+    err = plh::launch_pack_x(g, a, s);
+    if (err != hipSuccess) return fail_hip(err, "x packing");
+    err = plh::launch_recurrent(g, a, s);
+    if (err != hipSuccess) return fail_hip(err, "persistent LSTM launch");
+  }
+  return PLH_OK;
+}
+
+int plh_status(const void* workspace, uint32_t* status, void* stream) {
+  if (!workspace || !status) return fail(PLH_ERR_INVALID, "workspace and status are required");
+  hipError_t e = hipMemcpyAsync(status, workspace, sizeof(uint32_t), hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "status read");
+  return PLH_OK;
+}
+
+int plh_repeat_first_row(const void* in, void* out, int rows, int cols, void* stream) {
+  if (rows < 0 || cols < 0) return fail(PLH_ERR_INVALID, "rows and cols must be non-negative");
+  if ((rows > 0 && cols > 0) && (!in || !out)) return fail(PLH_ERR_INVALID, "in and out are required");
+  hipError_t e = plh::launch_repeat_first_row((const _Float16*)in, (_Float16*)out, rows, cols, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "repeat_first_row launch");
+  return PLH_OK;
+}
+
+}  // extern "C"

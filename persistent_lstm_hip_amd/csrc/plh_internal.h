@@ -1,0 +1,92 @@
+// plh_internal.h -- declarations shared by the kernels (plh_kernels.hip) and the C ABI (plh_capi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+namespace plh {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// Geometry of one model as the kernels see it.  H is padded to HP (a bucket the kernel is
+// instantiated for); padded hidden units carry zero weights and zero bias, so their gates are
+// i = f = o = 0.5, g = 0 and their c and h stay exactly 0: padding never changes real outputs.
+struct Geometry {
+  int I, H, L, O;
+  int HP;      // padded hidden size: 32, 64 or 128
+  int waves;   // HP / 16: one wave per 16 hidden units (its i, f, g, o gate columns)
+  int kci;     // input-part K chunks of 32 for layers >= 1 (= HP / 32)
+  int kc;      // K chunks per wave: input part + recurrent part (= 2 * kci)
+  int kc_in0;  // input-part K chunks layer 0 uses (= ceil(I / 32) <= kci)
+};
+
+// Fills *g; returns false (with the reason) for geometries the kernels do not implement.
+bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why);
+
+// Byte offsets of the packed-weight blob (all 256-byte aligned).
+struct PackedLayout {
+  size_t wpack;  // f16 [L][waves][kc][4 gates][64 lanes][8]: each lane's MFMA A fragments
+  size_t bias;   // f32 [L][4][HP]: b_ih + b_hh
+  size_t wlin;   // f32 [O][HP]
+  size_t blin;   // f32 [O]
+  size_t total;
+};
+PackedLayout packed_layout(const Geometry& g);
+
+// Workspace of one persistent launch (reused by successive batch chunks):
+//   status   u32                                   PLH_STATUS_* bits
+//   counters u32 [L][ntile]                        steps published per (layer, tile)
+//   xp       f16x8 [ntile][T][kc_in0][64]          x in B-fragment order (layer 0 input)
+//   hseq     f16x8 [L-1][ntile][T][kci][64]        h of layers 0..L-2 in B-fragment order
+struct WorkspaceLayout {
+  size_t status, counters, xp, hseq, total;
+  int chunk_rows;  // batch rows per persistent launch (co-residency bound), multiple of 16
+};
+WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows);
+
+struct ForwardArgs {
+  const _Float16* x;            // [B, T, I]
+  const int32_t* lengths;       // [B] or null
+  const _Float16* wpack;        // packed blob sections
+  const float* bias;
+  const float* wlin;
+  const float* blin;
+  f16x8_t* xp;                  // packed x, see WorkspaceLayout
+  f16x8_t* hseq;                // inter-layer hand-off, see WorkspaceLayout
+  uint32_t* counters;           // [L][ntile] steps published per (layer, tile)
+  uint32_t* status;             // PLH_STATUS_* bits
+  const _Float16* h0;           // [L, B, H] or null
+  const _Float16* c0;
+  _Float16* out;                // [B, O] or null
+  _Float16* out_seq;            // [B, T, H] or null
+  _Float16* h_n;                // [L, B, H] or null
+  _Float16* c_n;
+  const int32_t* probe_steps;   // [n_probe], strictly increasing
+  float* probe_h;               // [n_probe, L, B, H]
+  float* probe_c;
+  int n_probe;
+  int B, T, I, H, L, O;
+  int row0, row_end;            // batch rows [row0, row_end) handled by this launch
+  int rows_pad, ntile;          // rows_pad = 16 * ntile
+  int kc_in0;
+  int xcd_map;                  // 1: keep a tile's layer chain on one XCD
+};
+
+hipError_t launch_pack_layer(const Geometry& g, int layer, const _Float16* w_ih, const _Float16* w_hh,
+                             _Float16* wpack, hipStream_t s);
+hipError_t launch_pack_bias(const Geometry& g, int layer, const _Float16* b_ih, const _Float16* b_hh,
+                            float* bias, hipStream_t s);
+hipError_t launch_pack_linear(const Geometry& g, const _Float16* w, const _Float16* b, float* wlin,
+                              float* blin, hipStream_t s);
+hipError_t launch_pack_x(const Geometry& g, const ForwardArgs& a, hipStream_t s);
+hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t s);
+hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, int cols, hipStream_t s);
+
+// Co-resident workgroups of the persistent kernel on the current device (0 with *err set on error).
+int recurrent_capacity(const Geometry& g, hipError_t* err);
+hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s);
+
+}  // namespace plh

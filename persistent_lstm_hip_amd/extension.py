@@ -1,0 +1,380 @@
+"""Loader of the native library and its torch-facing front end.
+
+The native boundary is the C ABI in include/persistent_lstm_hip.h (library
+persistent_lstm_hip_amd/lib/libpersistent_lstm_hip.so), bound here with ctypes.  torch only supplies
+device memory and the current HIP stream.  `load_extension()` keeps the contract of the reference's
+loader (persistent_lstm_hip/extension.py:7-12): it returns the extension object, or None when the
+library cannot be loaded (the reason is kept in `load_error()`).  The model classes turn None into a
+loud RuntimeError; nothing falls back to a CPU path.
+
+The extension object also exposes the reference extension's function names
+(persistent_lstm_hip/csrc/bindings.cpp:154-165) with their tensor signatures, so code written
+against `persistent_lstm_hip_ext` keeps working.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from functools import lru_cache
+from typing import Dict, List, Optional, Sequence
+
+import torch
+
+from .build import LIB_PATH
+
+PLH_OK = 0
+PLH_ERR_INVALID = 1
+PLH_ERR_UNSUPPORTED = 2
+PLH_ERR_HIP = 3
+PLH_ERR_DEVICE = 4
+PLH_STATUS_TIMEOUT = 1
+
+_load_error: Optional[str] = None
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.plh_abi_version.restype = _i32
+    lib.plh_abi_version.argtypes = []
+    lib.plh_last_error.restype = ctypes.c_char_p
+    lib.plh_last_error.argtypes = []
+    lib.plh_supports.restype = _i32
+    lib.plh_supports.argtypes = [_i32] * 4
+    lib.plh_packed_bytes.restype = _i64
+    lib.plh_packed_bytes.argtypes = [_i32] * 4
+    lib.plh_pack_regressor.restype = _i32
+    lib.plh_pack_regressor.argtypes = [_i32] * 4 + [ctypes.POINTER(_vp)] * 4 + [_vp, _vp, _vp, _i64, _vp]
+    lib.plh_workspace_bytes.restype = _i64
+    lib.plh_workspace_bytes.argtypes = [_i32] * 6
+    lib.plh_forward.restype = _i32
+    lib.plh_forward.argtypes = (
+        [_vp] + [_i32] * 4 + [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp]
+    )
+    lib.plh_status.restype = _i32
+    lib.plh_status.argtypes = [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]
+    lib.plh_repeat_first_row.restype = _i32
+    lib.plh_repeat_first_row.argtypes = [_vp, _vp, _i32, _i32, _vp]
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class NativeLibrary:
+    """Torch-facing wrapper of the C ABI.  All tensors live on one HIP device."""
+
+    ABI_VERSION = 1
+
+    def __init__(self, lib: ctypes.CDLL):
+        self.lib = lib
+        self.path = LIB_PATH
+        self._workspaces: Dict[tuple, torch.Tensor] = {}
+
+    # ---- errors -------------------------------------------------------------------------------
+    def _check(self, rc: int, what: str) -> None:
+        if rc == PLH_OK:
+            return
+        msg = f"{what}: {self.lib.plh_last_error().decode(errors='replace')}"
+        if rc in (PLH_ERR_INVALID, PLH_ERR_UNSUPPORTED):
+            raise ValueError(msg)
+        raise RuntimeError(msg)
+
+    def last_error(self) -> str:
+        return self.lib.plh_last_error().decode(errors="replace")
+
+    # ---- geometry -----------------------------------------------------------------------------
+    def supports(self, input_size: int, hidden_size: int, num_layers: int, output_size: int) -> bool:
+        return bool(self.lib.plh_supports(input_size, hidden_size, num_layers, output_size))
+
+    def packed_bytes(self, input_size: int, hidden_size: int, num_layers: int, output_size: int) -> int:
+        n = self.lib.plh_packed_bytes(input_size, hidden_size, num_layers, output_size)
+        if n < 0:
+            raise ValueError(self.last_error())
+        return int(n)
+
+    def workspace_bytes(self, input_size, hidden_size, num_layers, output_size, batch, seq_len) -> int:
+        n = self.lib.plh_workspace_bytes(input_size, hidden_size, num_layers, output_size, batch, seq_len)
+        if n < 0:
+            raise ValueError(self.last_error())
+        return int(n)
+
+    # ---- packing ------------------------------------------------------------------------------
+    def pack(
+        self,
+        w_ih: Sequence[torch.Tensor],
+        w_hh: Sequence[torch.Tensor],
+        b_ih: Sequence[Optional[torch.Tensor]],
+        b_hh: Optional[Sequence[Optional[torch.Tensor]]],
+        lin_w: Optional[torch.Tensor],
+        lin_b: Optional[torch.Tensor],
+    ) -> torch.Tensor:
+        """Pack torch-layout parameters (any float dtype, one device) into the kernel's blob."""
+        L = len(w_ih)
+        if L == 0 or len(w_hh) != L or len(b_ih) != L:
+            raise ValueError("w_ih, w_hh and b_ih need one tensor per layer")
+        device = w_hh[0].device
+        if device.type != "cuda":
+            raise ValueError("weights must be on a HIP device")
+        H = int(w_hh[0].shape[1])
+        I = int(w_ih[0].shape[1])
+        O = 0 if lin_w is None else int(lin_w.shape[0])
+        half = lambda t: None if t is None else t.detach().to(device=device, dtype=torch.float16).contiguous()  # noqa: E731
+        for l in range(L):
+            k = I if l == 0 else H
+            if tuple(w_ih[l].shape) != (4 * H, k) or tuple(w_hh[l].shape) != (4 * H, H):
+                raise ValueError(f"layer {l}: expected weight_ih [{4 * H}, {k}] and weight_hh [{4 * H}, {H}]")
+            for b in (b_ih[l], None if b_hh is None else b_hh[l]):
+                if b is not None and tuple(b.shape) != (4 * H,):
+                    raise ValueError(f"layer {l}: expected biases of shape [{4 * H}]")
+        if lin_w is not None and tuple(lin_w.shape) != (O, H):
+            raise ValueError(f"linear weight must be [{O}, {H}]")
+        keep: List[torch.Tensor] = []
+
+        def arr(ts):
+            a = (_vp * L)()
+            for i, t in enumerate(ts):
+                h = half(t)
+                if h is not None:
+                    keep.append(h)
+                    a[i] = h.data_ptr()
+            return a
+
+        a_wih, a_whh, a_bih = arr(w_ih), arr(w_hh), arr(b_ih)
+        a_bhh = arr(b_hh) if b_hh is not None else None
+        lw, lb = half(lin_w), half(lin_b)
+        nbytes = self.packed_bytes(I, H, L, O)
+        packed = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        with torch.cuda.device(device):
+            rc = self.lib.plh_pack_regressor(
+                I, H, L, O, a_wih, a_whh, a_bih, a_bhh, _ptr(lw), _ptr(lb), packed.data_ptr(), nbytes,
+                _stream(device),
+            )
+        self._check(rc, "plh_pack_regressor")
+        # The fp16 copies in `keep` are read asynchronously; the caching allocator only hands their
+        # blocks to later work on the same stream, which runs after the pack kernels.
+        return packed
+
+    # ---- forward ------------------------------------------------------------------------------
+    def workspace(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        """A cached workspace of at least nbytes per (device, stream): calls on one stream are
+        ordered by it; calls on different streams get different workspaces."""
+        key = (device.type, device.index, _stream(device))
+        ws = self._workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            if ws.data_ptr() % 256:
+                ws = torch.empty(max(nbytes, 256) + 256, dtype=torch.uint8, device=device)
+                off = (-ws.data_ptr()) % 256
+                ws = ws[off:]
+            self._workspaces[key] = ws
+        return ws
+
+    def forward(
+        self,
+        packed: torch.Tensor,
+        dims: Sequence[int],
+        x: torch.Tensor,
+        *,
+        lengths: Optional[torch.Tensor] = None,
+        h0: Optional[torch.Tensor] = None,
+        c0: Optional[torch.Tensor] = None,
+        want_out: bool = True,
+        want_seq: bool = False,
+        want_state: bool = False,
+        probe_steps: Optional[Sequence[int]] = None,
+        check_status: bool = False,
+    ) -> Dict[str, torch.Tensor]:
+        """Run plh_forward.  dims = (I, H, L, O).  x: [B, T, I] on a HIP device (cast to fp16).
+
+        Returns a dict with "out" [B, O], "out_seq" [B, T, H], "h_n"/"c_n" [L, B, H] (fp16) and
+        "probe_h"/"probe_c" [P, L, B, H] (fp32), as requested.
+        """
+        I, H, L, O = (int(d) for d in dims)
+        if not isinstance(x, torch.Tensor) or x.dim() != 3:
+            raise ValueError("x must be a [batch, seq_len, input_size] tensor")
+        if x.device.type != "cuda":
+            raise ValueError("x must be on a HIP device: this library has no CPU path")
+        if int(x.size(2)) != I:
+            raise ValueError(f"x has input size {int(x.size(2))}, the model expects {I}")
+        if not x.is_floating_point():
+            raise ValueError("x must be a floating-point tensor")
+        device = x.device
+        B, T = int(x.size(0)), int(x.size(1))
+        xh = x.to(torch.float16).contiguous()
+        opts = dict(device=device, dtype=torch.float16)
+        out = torch.empty((B, O), **opts) if (want_out and O > 0) else None
+        out_seq = torch.empty((B, T, H), **opts) if want_seq else None
+        h_n = torch.empty((L, B, H), **opts) if want_state else None
+        c_n = torch.empty((L, B, H), **opts) if want_state else None
+        lens_dev = None
+        if lengths is not None:
+            lens = torch.as_tensor(lengths)
+            if lens.dim() != 1 or int(lens.numel()) != B:
+                raise ValueError("lengths must be a 1-D tensor with one entry per batch row")
+            lc = lens.detach().to("cpu", torch.int64)
+            if B and (int(lc.min()) < 0 or int(lc.max()) > T):
+                raise ValueError(f"lengths must lie in [0, {T}]")
+            lens_dev = lens.to(device=device, dtype=torch.int32).contiguous()
+        states = []
+        for s in (h0, c0):
+            if s is None:
+                states.append(None)
+                continue
+            if tuple(s.shape) != (L, B, H):
+                raise ValueError(f"initial states must be [{L}, {B}, {H}]")
+            states.append(s.to(**opts).contiguous())
+        probes = sorted(set(int(p) for p in (probe_steps or ())))
+        if probes and (probes[0] < 1 or probes[-1] > T):
+            raise ValueError(f"probe steps must lie in [1, {T}]")
+        P = len(probes)
+        probe_dev = torch.tensor(probes, dtype=torch.int32, device=device) if P else None
+        probe_h = torch.empty((P, L, B, H), device=device, dtype=torch.float32) if P else None
+        probe_c = torch.empty((P, L, B, H), device=device, dtype=torch.float32) if P else None
+        if packed.device != device:
+            raise ValueError("packed weights and x must be on the same device")
+        with torch.cuda.device(device):
+            nws = self.workspace_bytes(I, H, L, O, B, T)
+            ws = self.workspace(device, nws)
+            rc = self.lib.plh_forward(
+                packed.data_ptr(), I, H, L, O, _ptr(xh), B, T, _ptr(lens_dev), _ptr(states[0]), _ptr(states[1]),
+                _ptr(out), _ptr(out_seq), _ptr(h_n), _ptr(c_n), _ptr(probe_dev), P, _ptr(probe_h), _ptr(probe_c),
+                ws.data_ptr(), ws.numel(), _stream(device),
+            )
+            self._check(rc, "plh_forward")
+            if check_status:
+                self.check_status(device)
+        res: Dict[str, torch.Tensor] = {}
+        if out is not None:
+            res["out"] = out
+        if out_seq is not None:
+            res["out_seq"] = out_seq
+        if want_state:
+            res["h_n"], res["c_n"] = h_n, c_n
+        if P:
+            res["probe_h"], res["probe_c"] = probe_h, probe_c
+        return res
+
+    def status(self, device: torch.device) -> int:
+        """Synchronise the current stream and return the device status word of the last forward."""
+        ws = self._workspaces.get((device.type, device.index, _stream(device)))
+        if ws is None:
+            return 0
+        st = ctypes.c_uint32(0)
+        with torch.cuda.device(device):
+            self._check(self.lib.plh_status(ws.data_ptr(), ctypes.byref(st), _stream(device)), "plh_status")
+        return int(st.value)
+
+    def check_status(self, device: torch.device) -> None:
+        st = self.status(device)
+        if st & PLH_STATUS_TIMEOUT:
+            raise RuntimeError("persistent LSTM kernel: a layer hand-off wait timed out (outputs are invalid)")
+        if st:
+            raise RuntimeError(f"persistent LSTM kernel reported status {st:#x}")
+
+    # ---- reference extension surface (bindings.cpp:154-165) ----------------------------------
+    def repeat_first_row(self, inp: torch.Tensor, output_batch_size: int) -> torch.Tensor:
+        """bindings.cpp:164: out[r] = inp[0] for r < output_batch_size (fp16, HIP tensor)."""
+        if inp.dim() != 2 or inp.dtype != torch.float16 or inp.device.type != "cuda":
+            raise ValueError("repeat_first_row expects a 2-D float16 HIP tensor")
+        inp = inp.contiguous()
+        cols = int(inp.size(1))
+        out = torch.empty((int(output_batch_size), cols), dtype=inp.dtype, device=inp.device)
+        with torch.cuda.device(inp.device):
+            rc = self.lib.plh_repeat_first_row(inp.data_ptr(), out.data_ptr(), int(output_batch_size), cols,
+                                               _stream(inp.device))
+        self._check(rc, "plh_repeat_first_row")
+        return out
+
+    def persistent_lstm_regressor_forward_generic_projected(
+        self, x, weight_ih: List[torch.Tensor], weight_hh: List[torch.Tensor], bias: List[torch.Tensor],
+        linear_weight: torch.Tensor, linear_bias: torch.Tensor,
+    ) -> torch.Tensor:
+        """bindings.cpp:163: (x, [W_ih], [W_hh], [b_ih + b_hh], W_lin, b_lin) -> [B, O].  Packs per call."""
+        packed = self.pack(weight_ih, weight_hh, bias, None, linear_weight, linear_bias)
+        dims = (int(weight_ih[0].shape[1]), int(weight_hh[0].shape[1]), len(weight_ih), int(linear_weight.shape[0]))
+        return self.forward(packed, dims, x)["out"]
+
+    @staticmethod
+    def unpack_kpairs(packed: torch.Tensor, k: int) -> torch.Tensor:
+        """Invert the reference's kpairs layout P[p, c, j] = W[c, 2p + j] (model.py:20-27), as its CPU
+        branch does (persistent_lstm_op.cpp:161-168): returns W [4H, k]."""
+        if packed.dim() != 3 or packed.size(2) != 2:
+            raise ValueError("kpairs-packed weight must be [ceil(K/2), 4H, 2]")
+        pairs, out = int(packed.size(0)), int(packed.size(1))
+        full = packed.permute(0, 2, 1).reshape(pairs * 2, out)
+        return full[:k].t().contiguous()
+
+    def persistent_lstm4_forward_interleaved(self, x, *args) -> torch.Tensor:
+        """bindings.cpp:157: (x, W_ih_l0, W_hh_l0, b_l0, ..., W_ih_l3, W_hh_l3, b_l3, W_lin, b_lin) with
+        kpairs-packed weights (model.py:562-578) and fused biases."""
+        if len(args) != 14:
+            raise ValueError("expected 12 per-layer tensors plus linear weight and bias")
+        H = int(args[1].size(1)) // 4
+        I = int(x.size(2))
+        w_ih = [self.unpack_kpairs(args[3 * l], I if l == 0 else H) for l in range(4)]
+        w_hh = [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)]
+        bias = [args[3 * l + 2] for l in range(4)]
+        return self.persistent_lstm_regressor_forward_generic_projected(x, w_ih, w_hh, bias, args[12], args[13])
+
+    def persistent_lstm4_forward_projected(self, x, *args) -> torch.Tensor:
+        """bindings.cpp:158: native W_ih [4H, K] with kpairs-packed W_hh (model.py:548-560)."""
+        if len(args) != 14:
+            raise ValueError("expected 12 per-layer tensors plus linear weight and bias")
+        H = int(args[0].size(0)) // 4
+        w_ih = [args[3 * l] for l in range(4)]
+        w_hh = [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)]
+        bias = [args[3 * l + 2] for l in range(4)]
+        return self.persistent_lstm_regressor_forward_generic_projected(x, w_ih, w_hh, bias, args[12], args[13])
+
+    def persistent_lstm4_forward(self, x, *args) -> torch.Tensor:
+        """bindings.cpp:155: torch-layout weights and fused biases."""
+        if len(args) != 14:
+            raise ValueError("expected 12 per-layer tensors plus linear weight and bias")
+        return self.persistent_lstm_regressor_forward_generic_projected(
+            x, [args[3 * l] for l in range(4)], [args[3 * l + 1] for l in range(4)],
+            [args[3 * l + 2] for l in range(4)], args[12], args[13])
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+@lru_cache(maxsize=1)
+def load_extension() -> Optional[NativeLibrary]:
+    """The native library, or None if it cannot be loaded (see load_error())."""
+    global _load_error
+    if not os.path.exists(LIB_PATH):
+        _load_error = f"{LIB_PATH} is missing: run `python -m persistent_lstm_hip_amd.build`"
+        return None
+    try:
+        # torch ships the HIP runtime; loading it first lets the library bind to the same copy.
+        import torch.cuda  # noqa: F401
+
+        lib = ctypes.CDLL(LIB_PATH)
+        _declare(lib)
+        if lib.plh_abi_version() != NativeLibrary.ABI_VERSION:
+            _load_error = "ABI version mismatch between the library and its Python front end"
+            return None
+        return NativeLibrary(lib)
+    except OSError as exc:
+        _load_error = f"cannot load {LIB_PATH}: {exc}"
+        return None
+
+
+def load_error() -> Optional[str]:
+    return _load_error
+
+
+def require_extension() -> NativeLibrary:
+    """The native library; RuntimeError (never a fallback) if it is unavailable."""
+    ext = load_extension()
+    if ext is None:
+        raise RuntimeError(f"persistent_lstm_hip_amd native library unavailable: {_load_error}")
+    return ext

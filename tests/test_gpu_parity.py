@@ -1,0 +1,206 @@
+"""Parity of the HIP forward against the CPU oracle (oracle/lstm_oracle.c) and torch's fp32 nn.LSTM.
+
+Bar: max-abs <= 2e-2 and mean-abs <= 2e-3 on the [B, O] output, and the same
+bound on every layer's h and c after 1, 100 and 1000 steps.  The GPU runs fp16 weights (a .half()
+copy of the seeded fp32 model); the references run the original fp32 weights.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import (assert_close, linear_params, make_lengths, make_regressor, make_x, oracle_layers)
+from oracle import oracle
+from persistent_lstm_hip_amd import PersistentLSTM, PersistentLSTMRegressor, convert_regressor_module
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg: str) -> None:
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _gpu_model(native):
+    m = PersistentLSTMRegressor.from_native_module(native).to("cuda").half().eval()
+    return m
+
+
+def _torch_ref(native, x, lengths=None):
+    with torch.inference_mode():
+        if lengths is None:
+            return native(x).numpy()
+        packed = torch.nn.utils.rnn.pack_padded_sequence(x, lengths, batch_first=True, enforce_sorted=False)
+        _, (h, _) = native.lstm(packed)
+        return native.linear(h[-1]).numpy()
+
+
+@pytest.mark.parametrize("I,H,L,O,B,T", [
+    (5, 128, 1, 24, 8, 64),      # C1 shape
+    (5, 32, 2, 7, 20, 37),       # H bucket 32, ragged tile, T not a multiple of the chunk
+    (5, 64, 3, 24, 33, 19),      # H bucket 64
+    (17, 100, 2, 5, 16, 9),      # padded H and I > 8
+    (5, 128, 4, 24, 48, 130),    # headline geometry, small batch
+])
+def test_regressor_matches_oracle(gpu, I, H, L, O, B, T):
+    _say(f"regressor I={I} H={H} L={L} O={O} B={B} T={T}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear))
+    np.testing.assert_allclose(want, _torch_ref(native, x), atol=1e-5)
+    got = _gpu_model(native)(x.to("cuda", torch.float16))
+    gpu.check_status(torch.device("cuda"))
+    assert got.dtype == torch.float16 and tuple(got.shape) == (B, O)
+    assert_close(got.float().cpu().numpy(), want, what="out")
+
+
+def test_headline_c2_full_batch(gpu):
+    """C2: 4 layers, H128, B512, T1000.  Full output vs torch fp32 CPU; probes vs the oracle."""
+    I, H, L, O, B, T = 5, 128, 4, 24, 512, 1000
+    _say("C2 full batch")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    model = _gpu_model(native)
+    xg = x.to("cuda", torch.float16)
+    out, ph, pc = model.forward_probe(xg, [1, 100, 1000])
+    gpu.check_status(torch.device("cuda"))
+    out2 = model(xg)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "probe and plain forward disagree"
+    want = _torch_ref(native, x)
+    mx, mn = assert_close(out.float().cpu().numpy(), want, what="C2 out vs torch fp32")
+    _say(f"C2 out vs torch fp32: max_abs={mx:.3e} mean_abs={mn:.3e}")
+    rows = np.r_[0:16, 250:266, 496:512]
+    ref = oracle.lstm_forward(x.numpy()[rows], oracle_layers(native.lstm), probe_steps=(1, 100, 1000))
+    for p, step in enumerate((1, 100, 1000)):
+        for name, got_all, want_all in (("h", ph, ref["probe_h"]), ("c", pc, ref["probe_c"])):
+            g = got_all[p][:, rows].cpu().numpy()
+            mx, mn = assert_close(g, want_all[p], what=f"{name} after {step} steps")
+            _say(f"{name}@{step}: max_abs={mx:.3e} mean_abs={mn:.3e}")
+
+
+def test_ragged_c5(gpu):
+    """C5: lengths ~ U[200, 1000] sorted descending, packed-sequence semantics, head on h_n[-1]."""
+    I, H, L, O, B, T = 5, 128, 4, 24, 512, 1000
+    _say("C5 ragged")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    lengths = make_lengths(B, T, 200)
+    model = _gpu_model(native)
+    out = model.forward_ragged(x.to("cuda", torch.float16), lengths)
+    gpu.check_status(torch.device("cuda"))
+    want = _torch_ref(native, x, lengths)
+    mx, mn = assert_close(out.float().cpu().numpy(), want, what="C5 out vs packed torch")
+    _say(f"C5 vs packed torch: max_abs={mx:.3e} mean_abs={mn:.3e}")
+    rows = np.r_[0:16, 300:316, 496:512]
+    ref = oracle.regressor_forward(x.numpy()[rows], oracle_layers(native.lstm), *linear_params(native.linear),
+                                   lengths=lengths.numpy()[rows])
+    assert_close(out.float().cpu().numpy()[rows], ref, what="C5 out vs oracle")
+
+
+def test_ragged_small_unsorted_with_zero_length(gpu):
+    I, H, L, O, B, T = 5, 64, 2, 3, 21, 40
+    _say("ragged small unsorted")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    lengths = torch.randint(1, T + 1, (B,), generator=torch.Generator().manual_seed(5))
+    lengths[3] = 0
+    lengths[7] = T
+    model = _gpu_model(native)
+    got = model.forward_ragged(x.to("cuda", torch.float16), lengths).float().cpu().numpy()
+    want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
+                                    lengths=lengths.numpy())
+    assert_close(got, want, what="ragged small")
+    # a zero-length row never updates: the head sees h = 0
+    np.testing.assert_allclose(got[3], native.linear.bias.detach().numpy(), atol=2e-3)
+
+
+def test_persistent_lstm_dropin(gpu):
+    I, H, L, B, T = 5, 128, 2, 24, 50
+    _say("PersistentLSTM drop-in")
+    torch.manual_seed(7)
+    lstm = torch.nn.LSTM(I, H, L, batch_first=True).eval()
+    x = make_x(B, T, I, seed=3)
+    g = torch.Generator().manual_seed(4)
+    h0 = 0.5 * torch.randn(L, B, H, generator=g)
+    c0 = 0.5 * torch.randn(L, B, H, generator=g)
+    with torch.inference_mode():
+        want_out, (want_h, want_c) = lstm(x, (h0, c0))
+    mod = PersistentLSTM.from_native_module(lstm).to("cuda").half()
+    out, (h, c) = mod(x.to("cuda", torch.float16), (h0.cuda().half(), c0.cuda().half()))
+    gpu.check_status(torch.device("cuda"))
+    assert tuple(out.shape) == (B, T, H) and tuple(h.shape) == (L, B, H)
+    assert_close(out.float().cpu().numpy(), want_out.numpy(), what="out seq")
+    assert_close(h.float().cpu().numpy(), want_h.numpy(), what="h_n")
+    assert_close(c.float().cpu().numpy(), want_c.numpy(), what="c_n")
+    # PackedSequence input
+    lengths = torch.tensor(sorted(torch.randint(1, T + 1, (B,), generator=g).tolist(), reverse=True))
+    packed = torch.nn.utils.rnn.pack_padded_sequence(x, lengths, batch_first=True)
+    with torch.inference_mode():
+        wp, (wh, wc) = lstm(packed)
+    wpad, _ = torch.nn.utils.rnn.pad_packed_sequence(wp, batch_first=True, total_length=T)
+    gp = torch.nn.utils.rnn.pack_padded_sequence(x.to("cuda", torch.float16), lengths, batch_first=True)
+    op, (oh, oc) = mod(gp)
+    opad, _ = torch.nn.utils.rnn.pad_packed_sequence(op, batch_first=True, total_length=T)
+    assert_close(opad.float().cpu().numpy(), wpad.numpy(), what="packed out")
+    assert_close(oh.float().cpu().numpy(), wh.numpy(), what="packed h_n")
+    assert_close(oc.float().cpu().numpy(), wc.numpy(), what="packed c_n")
+
+
+def test_row_permutation_and_determinism(gpu):
+    I, H, L, O, B, T = 5, 128, 4, 24, 64, 200
+    _say("permutation + determinism")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I).to("cuda", torch.float16)
+    model = _gpu_model(native)
+    a = model(x)
+    b = model(x)
+    perm = torch.randperm(B, generator=torch.Generator().manual_seed(9)).cuda()
+    c = model(x[perm])
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), "two runs differ"
+    assert torch.equal(a[perm], c), "batch rows are not independent"
+
+
+def test_uniform_batch_shortcut(gpu):
+    I, H, L, O, B, T = 5, 128, 4, 24, 512, 300
+    _say("uniform batch")
+    native = make_regressor(I, H, L, O)
+    model = _gpu_model(native)
+    x = torch.ones(B, T, I, device="cuda", dtype=torch.float16)
+    out = model(x)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out[:1].expand_as(out))
+    want = _torch_ref(native, torch.ones(1, T, I))
+    assert_close(out[:1].float().cpu().numpy(), want, what="uniform row")
+
+
+def test_reference_extension_surface(gpu):
+    """The reference's extension entry points, fed the reference's packed formats."""
+    I, H, L, O, B, T = 5, 128, 4, 24, 32, 60
+    _say("extension surface")
+    native = make_regressor(I, H, L, O).to("cuda").half()
+    x = make_x(B, T, I).to("cuda", torch.float16)
+    lstm = native.lstm
+
+    def kpairs(w):  # P[p, c, j] = W[c, 2p + j], zero-padded to even K
+        k = w.shape[1]
+        wt = torch.nn.functional.pad(w.t(), (0, 0, 0, k % 2))
+        return wt.reshape(-1, 2, w.shape[0]).permute(0, 2, 1).contiguous()
+
+    fused = [getattr(lstm, f"bias_ih_l{l}") + getattr(lstm, f"bias_hh_l{l}") for l in range(L)]
+    w_ih = [getattr(lstm, f"weight_ih_l{l}") for l in range(L)]
+    w_hh = [getattr(lstm, f"weight_hh_l{l}") for l in range(L)]
+    want = convert_regressor_module(native)(x)
+    a = gpu.persistent_lstm_regressor_forward_generic_projected(x, w_ih, w_hh, fused, native.linear.weight,
+                                                                native.linear.bias)
+    args = []
+    for l in range(L):
+        args += [kpairs(w_ih[l]), kpairs(w_hh[l]), fused[l]]
+    b = gpu.persistent_lstm4_forward_interleaved(x, *args, native.linear.weight, native.linear.bias)
+    r = gpu.repeat_first_row(a[:1], 7)
+    torch.cuda.synchronize()
+    # the reference fuses the bias in fp16 before the kernel: allow that rounding
+    assert_close(a.float().cpu().numpy(), want.float().cpu().numpy(), max_abs=2e-3, mean_abs=5e-4, what="generic")
+    assert torch.equal(a, b)
+    assert torch.equal(r, a[:1].expand(7, -1))

@@ -104,6 +104,17 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
  * (0 = success, else PLH_STATUS_* bits).  Returns PLH_OK or PLH_ERR_HIP. */
 int plh_status(const void* workspace, uint32_t* status, void* stream);
 
+/*
+ * Optional timing of the persistent kernel alone (for benchmarks and profilers of the caller).
+ * plh_kernel_timing(n) with n > 0 arms n pairs of HIP events for the calling thread: each later
+ * plh_forward on this thread records one pair around its persistent launch(es), until the n pairs
+ * are used.  plh_kernel_timing(0) disarms.  plh_kernel_timing_read synchronises on the recorded
+ * events and returns the summed elapsed milliseconds and the number of timed forwards.
+ * No counterpart in the reference (it only timed whole forwards from Python, LSTM-hip.py:80-91).
+ */
+int plh_kernel_timing(int max_forwards);
+int plh_kernel_timing_read(double* total_ms, int* forwards);
+
 /* out[r, c] = in[0, c] for r < rows (fp16).  Replaces repeat_first_row
  * (bindings.cpp:164, persistent_lstm_hip.cu:1684-1695, :1784-1809). */
 int plh_repeat_first_row(const void* in, void* out, int rows, int cols, void* stream);

@@ -17,6 +17,7 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpersistent_lstm_hip.so")
+BENCH_PATH = os.path.join(LIB_DIR, "plh_bench")
 SOURCES = ["plh_kernels.hip", "plh_capi.hip"]
 HEADERS = ["plh_internal.h", os.path.join("..", "..", "include", "persistent_lstm_hip.h")]
 
@@ -55,6 +56,15 @@ def build(verbose: bool = False) -> str:
     if verbose and out.strip():
         print(out)
     os.replace(tmp, LIB_PATH)
+    # Native driver of the C ABI (profiling target and integration example), linked to the library.
+    cmd = [hipcc(), "-O2", "-std=c++17", os.path.join(CSRC, "plh_bench_main.cpp"), "-L" + LIB_DIR,
+           "-lpersistent_lstm_hip", "-Wl,-rpath,$ORIGIN", "-o", BENCH_PATH + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc (plh_bench) failed ({proc.returncode}):\n{proc.stdout}")
+    os.replace(BENCH_PATH + ".tmp", BENCH_PATH)
     return LIB_PATH
 
 

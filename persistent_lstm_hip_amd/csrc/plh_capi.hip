@@ -12,6 +12,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "plh_internal.h"
 #include "../../include/persistent_lstm_hip.h"
@@ -74,6 +75,19 @@ int geometry_code(int I, int H, int L, int O) {
 }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Armed timing events of the calling thread (plh_kernel_timing).
+struct KernelTiming {
+  std::vector<hipEvent_t> ev;  // begin/end pairs
+  int used = 0;                // pairs recorded
+  ~KernelTiming() { release(); }
+  void release() {
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    ev.clear();
+    used = 0;
+  }
+};
+thread_local KernelTiming g_timing;
 
 }  // namespace
 
@@ -206,6 +220,7 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   a.O = g.O;
   a.kc_in0 = g.kc_in0;
 
+  const bool timed = g_timing.used * 2 < (int)g_timing.ev.size();
   for (int row0 = 0; row0 < batch; row0 += chunk_rows) {
     const int rows = std::min(chunk_rows, batch - row0);
     a.row0 = row0;
@@ -217,9 +232,48 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     if (err != hipSuccess) return fail_hip(err, "counter reset");
     err = plh::launch_pack_x(g, a, s);
     if (err != hipSuccess) return fail_hip(err, "x packing");
+    if (timed && row0 == 0) {
+      err = hipEventRecord(g_timing.ev[2 * g_timing.used], s);
+      if (err != hipSuccess) return fail_hip(err, "timing event");
+    }
     err = plh::launch_recurrent(g, a, s);
     if (err != hipSuccess) return fail_hip(err, "persistent LSTM launch");
   }
+  if (timed) {
+    err = hipEventRecord(g_timing.ev[2 * g_timing.used + 1], s);
+    if (err != hipSuccess) return fail_hip(err, "timing event");
+    ++g_timing.used;
+  }
+  return PLH_OK;
+}
+
+int plh_kernel_timing(int max_forwards) {
+  g_timing.release();
+  if (max_forwards < 0) return fail(PLH_ERR_INVALID, "max_forwards must be non-negative");
+  for (int i = 0; i < 2 * max_forwards; ++i) {
+    hipEvent_t e;
+    hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) {
+      g_timing.release();
+      return fail_hip(err, "timing event creation");
+    }
+    g_timing.ev.push_back(e);
+  }
+  return PLH_OK;
+}
+
+int plh_kernel_timing_read(double* total_ms, int* forwards) {
+  if (!total_ms || !forwards) return fail(PLH_ERR_INVALID, "total_ms and forwards are required");
+  double sum = 0.0;
+  for (int i = 0; i < g_timing.used; ++i) {
+    float ms = 0.0f;
+    hipError_t err = hipEventSynchronize(g_timing.ev[2 * i + 1]);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, g_timing.ev[2 * i], g_timing.ev[2 * i + 1]);
+    if (err != hipSuccess) return fail_hip(err, "timing read");
+    sum += ms;
+  }
+  *total_ms = sum;
+  *forwards = g_timing.used;
   return PLH_OK;
 }
 

@@ -590,8 +590,11 @@ hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, 
   return hipGetLastError();
 }
 
-// Steps per hand-off chunk.
-constexpr int kChunk = 8;
+// Steps per hand-off chunk (compile-time tuning knob).
+#ifndef PLH_CHUNK_STEPS
+#define PLH_CHUNK_STEPS 8
+#endif
+constexpr int kChunk = PLH_CHUNK_STEPS;
 
 static const void* recurrent_kernel(const Geometry& g) {
   switch (g.HP) {

@@ -20,7 +20,8 @@ from typing import Dict, List, Optional, Sequence
 
 import torch
 
-from .build import LIB_PATH
+# Built by persistent_lstm_hip_amd/build.py.
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libpersistent_lstm_hip.so")
 
 PLH_OK = 0
 PLH_ERR_INVALID = 1
@@ -55,6 +56,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     )
     lib.plh_status.restype = _i32
     lib.plh_status.argtypes = [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]
+    lib.plh_kernel_timing.restype = _i32
+    lib.plh_kernel_timing.argtypes = [_i32]
+    lib.plh_kernel_timing_read.restype = _i32
+    lib.plh_kernel_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i32)]
     lib.plh_repeat_first_row.restype = _i32
     lib.plh_repeat_first_row.argtypes = [_vp, _vp, _i32, _i32, _vp]
 
@@ -277,6 +282,18 @@ class NativeLibrary:
             raise RuntimeError("persistent LSTM kernel: a layer hand-off wait timed out (outputs are invalid)")
         if st:
             raise RuntimeError(f"persistent LSTM kernel reported status {st:#x}")
+
+    # ---- timing of the persistent kernel alone ----------------------------------------------
+    def kernel_timing(self, max_forwards: int) -> None:
+        """Arm HIP events around the persistent launch of the next max_forwards forwards (this thread)."""
+        self._check(self.lib.plh_kernel_timing(int(max_forwards)), "plh_kernel_timing")
+
+    def kernel_timing_read(self):
+        """(summed kernel milliseconds, number of timed forwards); synchronises on the events."""
+        ms = ctypes.c_double(0.0)
+        n = _i32(0)
+        self._check(self.lib.plh_kernel_timing_read(ctypes.byref(ms), ctypes.byref(n)), "plh_kernel_timing_read")
+        return float(ms.value), int(n.value)
 
     # ---- reference extension surface (bindings.cpp:154-165) ----------------------------------
     def repeat_first_row(self, inp: torch.Tensor, output_batch_size: int) -> torch.Tensor:

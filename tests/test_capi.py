@@ -1,0 +1,114 @@
+"""The C ABI library: it loads, exports every function include/persistent_lstm_hip.h declares, and its
+host-side logic (geometry rules, sizes, argument validation) behaves - no device work on the CPU."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from persistent_lstm_hip_amd.extension import (PLH_ERR_INVALID, PLH_ERR_UNSUPPORTED, PLH_OK, LIB_PATH,
+                                               load_extension, load_error)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "persistent_lstm_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(plh_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def ext():
+    e = load_extension()
+    assert e is not None, load_error()
+    return e
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for must in ("plh_forward", "plh_pack_regressor", "plh_workspace_bytes", "plh_packed_bytes", "plh_supports",
+                 "plh_status", "plh_repeat_first_row", "plh_last_error", "plh_abi_version"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(ext):
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (plh_[a-z0-9_]+)", out))
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    for n in declared_functions():
+        assert hasattr(ext.lib, n)
+
+
+def test_abi_version_and_error_text(ext):
+    assert ext.lib.plh_abi_version() == 1
+    assert ext.lib.plh_supports(5, 4096, 4, 24) == 0
+    assert "hidden_size" in ext.last_error()
+
+
+@pytest.mark.parametrize("I,H,L,O,ok", [
+    (5, 128, 4, 24, True), (5, 1, 1, 1, True), (32, 32, 2, 0, True), (64, 64, 8, 3, True), (128, 128, 1, 24, True),
+    (5, 129, 4, 24, False), (33, 32, 2, 4, False), (0, 128, 4, 24, False), (5, 128, 0, 24, False), (5, 128, 4, -1, False),
+])
+def test_supported_geometries(ext, I, H, L, O, ok):
+    assert ext.supports(I, H, L, O) is ok
+
+
+def test_packed_bytes_closed_form(ext):
+    # wpack: L * (HP/16 waves) * (2*HP/32 chunks) * 4 gates * 64 lanes * 16 B, then f32 bias, head, all 256-aligned
+    a = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    for I, H, L, O, HP in [(5, 128, 4, 24, 128), (5, 100, 2, 3, 128), (5, 40, 3, 7, 64), (5, 10, 1, 0, 32)]:
+        wp = L * (HP // 16) * (HP // 16) * 4 * 64 * 16
+        want = a(wp) + a(L * 4 * HP * 4) + a(O * HP * 4) + a(O * 4)
+        assert ext.packed_bytes(I, H, L, O) == want
+    with pytest.raises(ValueError):
+        ext.packed_bytes(5, 1000, 4, 24)
+
+
+def test_workspace_bytes_grow_with_sequence(ext):
+    a = ext.workspace_bytes(5, 128, 4, 24, 512, 100)
+    b = ext.workspace_bytes(5, 128, 4, 24, 512, 1000)
+    assert 0 < a < b
+    # hand-off buffer dominates: (L-1) * rows * T * H * 2 bytes
+    assert b >= 3 * 512 * 1000 * 128 * 2
+    with pytest.raises(ValueError):
+        ext.workspace_bytes(5, 128, 4, 24, -1, 10)
+
+
+def test_forward_validates_before_touching_the_device(ext):
+    f = ext.lib.plh_forward
+    ws = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    # unsupported geometry
+    assert f(ws, 5, 999, 4, 24, ws, 4, 4, None, None, None, None, None, None, None, None, 0, None, None, ws, 1 << 20,
+             None) == PLH_ERR_UNSUPPORTED
+    # missing packed weights
+    assert f(None, 5, 128, 4, 24, ws, 4, 4, None, None, None, None, None, None, None, None, 0, None, None, ws, 1 << 20,
+             None) == PLH_ERR_INVALID
+    # probes requested without buffers
+    assert f(ws, 5, 128, 4, 24, ws, 4, 4, None, None, None, None, None, None, None, None, 2, None, None, ws, 1 << 20,
+             None) == PLH_ERR_INVALID
+    # misaligned workspace
+    assert f(ws, 5, 128, 4, 24, ws, 4, 4, None, None, None, None, None, None, None, None, 0, None, None,
+             ctypes.c_void_p(258), 1 << 20, None) == PLH_ERR_INVALID
+    assert ext.lib.plh_repeat_first_row(None, None, -1, 3, None) == PLH_ERR_INVALID
+    assert ext.lib.plh_repeat_first_row(None, None, 0, 0, None) == PLH_OK
+
+
+def test_pack_validates_before_touching_the_device(ext):
+    p = ext.lib.plh_pack_regressor
+    arr = (ctypes.c_void_p * 4)()
+    assert p(5, 128, 4, 24, arr, arr, arr, None, None, None, None, 0, None) == PLH_ERR_INVALID
+    assert p(5, 128, 4, 24, arr, arr, arr, None, None, None, ctypes.c_void_p(256), 1 << 30, None) == PLH_ERR_INVALID
+    assert p(5, 256 * 8, 4, 24, arr, arr, arr, None, None, None, None, 0, None) == PLH_ERR_UNSUPPORTED
+
+
+def test_kernel_timing_arming_without_forwards(ext):
+    assert ext.lib.plh_kernel_timing(0) == PLH_OK
+    ms, n = ext.kernel_timing_read()
+    assert n == 0 and ms == 0.0
+    assert ext.lib.plh_kernel_timing(-1) == PLH_ERR_INVALID

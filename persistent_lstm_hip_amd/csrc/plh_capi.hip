@@ -30,35 +30,63 @@ int fail_hip(hipError_t e, const char* what) {
   return fail(PLH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// Co-resident workgroup capacity per (device, HP), queried once.
+// Co-resident workgroup capacity per (device, HP, tile rows), queried once.
 std::mutex g_cap_mu;
 std::unordered_map<long long, int> g_cap;
 
-int capacity(const plh::Geometry& g, hipError_t* err) {
+int capacity(const plh::Geometry& g, int tile_rows, hipError_t* err) {
   int dev = 0;
   *err = hipGetDevice(&dev);
   if (*err != hipSuccess) return 0;
-  const long long key = (long long)dev * 4096 + g.HP;
+  const long long key = ((long long)dev * 4096 + g.HP) * 64 + tile_rows;
   {
     std::lock_guard<std::mutex> lk(g_cap_mu);
     auto it = g_cap.find(key);
     if (it != g_cap.end()) return it->second;
   }
-  const int c = plh::recurrent_capacity(g, err);
+  const int c = plh::recurrent_capacity(g, tile_rows, err);
   if (*err != hipSuccess) return 0;
   std::lock_guard<std::mutex> lk(g_cap_mu);
   g_cap[key] = c;
   return c;
 }
 
-// Rows per persistent launch: every (layer, tile) workgroup of a launch must be co-resident.
-// Without a device (capacity unknown) the plan assumes one workgroup per CU of a 256-CU MI355X.
-int plan_chunk_rows(const plh::Geometry& g, int batch, int cap) {
-  const int tiles_total = (batch + 15) / 16;
-  int tiles = cap / g.L;
+// Launch plan: every (layer, tile) workgroup of one persistent launch must be co-resident.
+// 8-row tiles halve the gate math per workgroup and are used when the whole batch fits one launch
+// with them; otherwise 16-row tiles, and the batch is split into sequential launches if needed.
+struct Plan {
+  int tile_rows = 16;
+  int chunk_rows = 16;
+};
+
+Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
+  Plan p;
+  batch = std::max(batch, 1);
+  const int tiles8 = (batch + 7) / 8;
+  if ((long long)g.L * tiles8 <= cap8) {
+    p.tile_rows = 8;
+    p.chunk_rows = tiles8 * 8;
+    return p;
+  }
+  int tiles = cap16 / g.L;
   if (tiles >= 8) tiles &= ~7;  // keep the XCD-aware mapping available
-  tiles = std::max(1, std::min(tiles, tiles_total));
-  return tiles * 16;
+  tiles = std::max(1, std::min(tiles, (batch + 15) / 16));
+  p.tile_rows = 16;
+  p.chunk_rows = tiles * 16;
+  return p;
+}
+
+// Plan on the current device; without one (capacity unknown) assume one workgroup per CU of a
+// 256-CU MI355X.
+Plan plan_for(const plh::Geometry& g, int batch, bool need_device, hipError_t* err) {
+  int cap8 = capacity(g, 8, err);
+  int cap16 = *err == hipSuccess ? capacity(g, 16, err) : 0;
+  if (*err != hipSuccess) {
+    if (need_device) return Plan();
+    cap8 = cap16 = 256;
+    *err = hipSuccess;
+  }
+  return make_plan(g, batch, cap8, cap16);
 }
 
 bool geometry(int I, int H, int L, int O, plh::Geometry* g) {
@@ -147,10 +175,8 @@ int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int
     return -1;
   }
   hipError_t err = hipSuccess;
-  int cap = capacity(g, &err);
-  if (err != hipSuccess || cap <= 0) cap = 256;  // planning without a device: 1 WG per CU, 256 CUs
-  const int rows = plan_chunk_rows(g, std::max(batch, 1), cap);
-  return (int64_t)plh::workspace_layout(g, seq_len, rows).total;
+  const Plan p = plan_for(g, batch, false, &err);
+  return (int64_t)plh::workspace_layout(g, seq_len, p.chunk_rows, p.tile_rows).total;
 }
 
 int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num_layers, int output_size,
@@ -170,13 +196,13 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   hipStream_t s = (hipStream_t)stream;
 
   hipError_t err = hipSuccess;
-  const int cap = capacity(g, &err);
+  const Plan plan = plan_for(g, batch, true, &err);
   if (err != hipSuccess) return fail_hip(err, "occupancy query");
-  if (cap < g.L)
+  if (capacity(g, 16, &err) < g.L)
     return fail(PLH_ERR_UNSUPPORTED, "the device cannot hold one workgroup per layer co-resident (layers = " +
-                                         std::to_string(g.L) + ", capacity = " + std::to_string(cap) + ")");
-  const int chunk_rows = plan_chunk_rows(g, std::max(batch, 1), cap);
-  const plh::WorkspaceLayout w = plh::workspace_layout(g, seq_len, chunk_rows);
+                                         std::to_string(g.L) + ")");
+  const int chunk_rows = plan.chunk_rows;
+  const plh::WorkspaceLayout w = plh::workspace_layout(g, seq_len, chunk_rows, plan.tile_rows);
   if (workspace_bytes < (int64_t)w.total)
     return fail(PLH_ERR_INVALID, "workspace smaller than plh_workspace_bytes()");
 
@@ -225,8 +251,9 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     const int rows = std::min(chunk_rows, batch - row0);
     a.row0 = row0;
     a.row_end = row0 + rows;
-    a.ntile = (rows + 15) / 16;
-    a.rows_pad = a.ntile * 16;
+    a.tile_rows = plan.tile_rows;
+    a.ntile = (rows + plan.tile_rows - 1) / plan.tile_rows;
+    a.rows_pad = a.ntile * plan.tile_rows;
     a.xcd_map = (a.ntile % 8 == 0) ? 1 : 0;
     err = plh::launch_zero_u32(counters, (size_t)g.L * a.ntile, s);
     if (err != hipSuccess) return fail_hip(err, "counter reset");

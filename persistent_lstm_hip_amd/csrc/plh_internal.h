@@ -36,16 +36,17 @@ struct PackedLayout {
 };
 PackedLayout packed_layout(const Geometry& g);
 
-// Workspace of one persistent launch (reused by successive batch chunks):
+// Workspace of one persistent launch (reused by successive batch chunks); R = rows per tile:
 //   status   u32                                   PLH_STATUS_* bits
 //   counters u32 [L][ntile]                        steps published per (layer, tile)
-//   xp       f16x8 [ntile][T][kc_in0][64]          x in B-fragment order (layer 0 input)
-//   hseq     f16x8 [L-1][ntile][T][kci][64]        h of layers 0..L-2 in B-fragment order
+//   xp       f16x8 [ntile][T][kc_in0][4][R]        x in B-fragment order (layer 0 input)
+//   hseq     f16x8 [L-1][ntile][T][kci][4][R]      h of layers 0..L-2 in B-fragment order
 struct WorkspaceLayout {
   size_t status, counters, xp, hseq, total;
-  int chunk_rows;  // batch rows per persistent launch (co-residency bound), multiple of 16
+  int chunk_rows;  // batch rows per persistent launch (co-residency bound), multiple of tile_rows
+  int tile_rows;   // batch rows per workgroup: 8 or 16
 };
-WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows);
+WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows, int tile_rows);
 
 struct ForwardArgs {
   const _Float16* x;            // [B, T, I]
@@ -70,7 +71,8 @@ struct ForwardArgs {
   int n_probe;
   int B, T, I, H, L, O;
   int row0, row_end;            // batch rows [row0, row_end) handled by this launch
-  int rows_pad, ntile;          // rows_pad = 16 * ntile
+  int rows_pad, ntile;          // rows_pad = tile_rows * ntile
+  int tile_rows;                // batch rows per workgroup: 8 or 16
   int kc_in0;
   int xcd_map;                  // 1: keep a tile's layer chain on one XCD
 };
@@ -86,7 +88,7 @@ hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t s);
 hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, int cols, hipStream_t s);
 
 // Co-resident workgroups of the persistent kernel on the current device (0 with *err set on error).
-int recurrent_capacity(const Geometry& g, hipError_t* err);
+int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err);
 hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s);
 
 }  // namespace plh

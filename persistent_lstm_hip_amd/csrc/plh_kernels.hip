@@ -39,16 +39,29 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.4426950408889634f;
 // Wall-clock bound on one hand-off wait (s_memrealtime runs at 100 MHz): 2 s.
 constexpr uint64_t kSpinLimitTicks = 200000000ull;
-constexpr int kFrag = 64;  // f16x8 elements in one 16 x 32 fragment block (1 KB)
 
-// logistic(x) = 1 / (1 + e^-x), with e^-x = 2^(-x log2 e) on v_exp_f32 and the reciprocal on
-// v_rcp_f32.  Saturates cleanly: exp2 -> inf gives 0, exp2 -> 0 gives 1.
-__device__ __forceinline__ float sigmoid_fast(float x) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+// e^{-k z} as 2^(min(-k z log2 e, 40)) on v_exp_f32.  The cap keeps a product of three (1 + e)
+// factors below 2^121 (no overflow) and moves no gate by more than 1e-12 (logistic(-27.7) ~ 1e-12).
+constexpr float kExpCap = 40.0f;
+__device__ __forceinline__ float exp_neg(float z, float k) {
+  return __builtin_amdgcn_exp2f(fminf(z * (-k * kLog2e), kExpCap));
 }
 
-// tanh(x) = 2 logistic(2x) - 1.
-__device__ __forceinline__ float tanh_fast(float x) { return fmaf(2.0f, sigmoid_fast(2.0f * x), -1.0f); }
+// One LSTM cell update (torch gate order i, f, g, o) from the pre-activations and the old c, with
+// 5 exponentials and 2 reciprocals instead of the 10 transcendentals of evaluating each of
+// sigmoid(i), sigmoid(f), tanh(g), sigmoid(o), tanh(c') as 1 / (1 + e^-x):
+//   c' = sigmoid(f) c + sigmoid(i) tanh(g) = [c (1+ei)(1+eg) + (1-eg)(1+ef)] / [(1+ef)(1+ei)(1+eg)]
+//   h  = sigmoid(o) tanh(c')               = (1 - ec) / [(1+eo)(1+ec)]
+// where ex = e^{-x} for the logistic gates and e^{-2x} for the tanh arguments.
+__device__ __forceinline__ void lstm_cell(float zi, float zf, float zg, float zo, float& c, float& h) {
+  const float ei = exp_neg(zi, 1.0f), ef = exp_neg(zf, 1.0f), eg = exp_neg(zg, 2.0f), eo = exp_neg(zo, 1.0f);
+  const float a = 1.0f + ei, b = 1.0f + eg, d = 1.0f + ef;
+  const float ab = a * b;
+  const float cn = fmaf(c, ab, (1.0f - eg) * d) * __builtin_amdgcn_rcpf(d * ab);
+  const float ec = exp_neg(cn, 2.0f);
+  h = (1.0f - ec) * __builtin_amdgcn_rcpf((1.0f + eo) * (1.0f + ec));
+  c = cn;
+}
 
 // Barrier that orders LDS traffic only: global stores stay in flight across it.
 __device__ __forceinline__ void lds_barrier() {
@@ -56,9 +69,6 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
-
-// Index (in halfs) of element (row r, k) inside a fragment-ordered [16 x K] block.
-__device__ __forceinline__ int frag_index(int r, int k) { return (((k >> 3) << 4) + r) * 8 + (k & 7); }
 
 // Spin (one lane) until *ctr >= need, bounded in wall-clock time, then acquire at agent scope.
 // Returns 0 if the wait timed out or any workgroup of the grid has failed.
@@ -95,35 +105,50 @@ __device__ __forceinline__ void block_coords(int b, int ntile, int xcd_map, int&
   }
 }
 
-template <int HP>
+template <int HP, int ROWS, int CH>
 struct Tile {
+  static_assert(ROWS == 8 || ROWS == 16, "tiles hold 8 or 16 batch rows");
   static constexpr int kWaves = HP / 16;
   static constexpr int kThreads = kWaves * 64;
-  static constexpr int kKci = HP / 32;  // input-part K chunks (layers >= 1)
-  static constexpr int kKcr = HP / 32;  // recurrent K chunks
+  static constexpr int kKci = HP / 32;          // input-part K chunks (layers >= 1)
+  static constexpr int kKcr = HP / 32;          // recurrent K chunks
   static constexpr int kKc = kKci + kKcr;
+  static constexpr int kFragVec = 4 * ROWS;     // f16x8 per [ROWS x 32] fragment block
+  static constexpr int kUpl = ROWS / 4;         // (unit, row) pairs per lane in the epilogue
+  // f16x8 elements each thread moves per chunk (input ring fill, hand-off copy)
+  static constexpr int kRn = (CH * kKci * kFragVec + kThreads - 1) / kThreads;
 };
 
-template <int HP, int CH>
-__global__ void __launch_bounds__(Tile<HP>::kThreads)
-lstm_wavefront_kernel(ForwardArgs a) {
-  using C = Tile<HP>;
-  constexpr int KCI = C::kKci, KCR = C::kKcr, KC = C::kKc, NT = C::kThreads;
-  constexpr int RN = (CH * KCI * kFrag + NT - 1) / NT;  // chunk elements held per thread
+// Offset (in halfs) of element (row r, k) in a fragment-ordered [ROWS x K] block: the block of K
+// chunk k/32 is stored as [k/8 % 4][row][8], i.e. exactly the B operand of one MFMA.
+template <int ROWS>
+__device__ __forceinline__ int frag_index(int r, int k) { return ((k >> 3) * ROWS + r) * 8 + (k & 7); }
 
-  __shared__ f16x8 ring[CH * KCI * kFrag];  // step inputs of the current chunk, fragment order
-  __shared__ f16x8 hfrag[2][KCR * kFrag];   // h_{t-1} / h_t, fragment order
+// The persistent layer-wavefront recurrence.  Template: padded hidden size HP, batch rows per
+// workgroup ROWS (16, or 8 with the MFMA's B columns 8..15 duplicating rows 0..7 so each lane
+// evaluates two (unit, row) pairs instead of four), steps per hand-off chunk CH.
+template <int HP, int ROWS, int CH>
+__global__ void __launch_bounds__(HP / 16 * 64)
+lstm_wavefront_kernel(ForwardArgs a) {
+  using C = Tile<HP, ROWS, CH>;
+  constexpr int KCI = C::kKci, KCR = C::kKcr, KC = C::kKc, NT = C::kThreads, FV = C::kFragVec;
+  constexpr int UPL = C::kUpl, RN = C::kRn;
+
+  __shared__ f16x8 ring[CH * KCI * FV];   // step inputs of the current chunk
+  __shared__ f16x8 hist[CH * KCR * FV];   // h of the chunk's steps; slot (t-1) % CH feeds step t
   __shared__ int s_ok[2];
   __shared__ int s_tlen;
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int n = lane & 15;   // batch row in the tile: B-operand / D column
-  const int kg = lane >> 4;  // K group of the A/B fragments, row group of D
+  const int n = lane & 15;            // B-operand / D column
+  const int kg = lane >> 4;           // K group of the A/B fragments, row group of D
+  const int r = n & (ROWS - 1);       // batch row in the tile
+  const int fl = kg * ROWS + r;       // this lane's B fragment within a block
   int layer, tile;
   block_coords(blockIdx.x, a.ntile, a.xcd_map, layer, tile);
 
-  const int grow = a.row0 + tile * 16 + n;
+  const int grow = a.row0 + tile * ROWS + r;
   const bool row_ok = grow < a.row_end;
   int len = 0;
   if (row_ok) {
@@ -139,39 +164,43 @@ lstm_wavefront_kernel(ForwardArgs a) {
   // Resident weights: A fragments of [W_ih | W_hh] rows for this wave's 16 units, 4 gates.
   f16x8 w[KC][4];
   {
-    const f16x8* wp = reinterpret_cast<const f16x8*>(a.wpack) + ((size_t)(layer * C::kWaves + wave) * KC * 4) * kFrag + lane;
+    const f16x8* wp = reinterpret_cast<const f16x8*>(a.wpack) + ((size_t)(layer * C::kWaves + wave) * KC * 4) * 64 + lane;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * kFrag];
+      for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
   }
-  const int u0 = wave * 16 + kg * 4;  // this lane's 4 hidden units: D rows 4*kg .. 4*kg+3
+  // D rows of this lane: units u0 .. u0+3 of row n; it evaluates UPL of them, starting at uo.
+  const int u0 = wave * 16 + kg * 4;
+  const int ibase = (ROWS == 8 && n >= 8) ? 2 : 0;
+  const int uo = u0 + ibase;
   f32x4 bias[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) bias[q] = *reinterpret_cast<const f32x4*>(a.bias + ((size_t)layer * 4 + q) * HP + u0);
 
-  // Initial state (nn.LSTM hx) or zeros; h_{-1} goes to hfrag[0].
-  float c[4];
-  f16x4 hcur;
+  // Initial state (nn.LSTM hx) or zeros; h_{-1} goes to history slot CH-1.
+  typedef _Float16 hvec __attribute__((ext_vector_type(UPL)));
+  float c[UPL];
+  hvec hcur;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int u = u0 + i;
+  for (int j = 0; j < UPL; ++j) {
+    const int u = uo + j;
     const bool v = row_ok && u < a.H;
     const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
-    c[i] = (v && a.c0) ? (float)a.c0[si] : 0.0f;
-    hcur[i] = (v && a.h0) ? a.h0[si] : (_Float16)0.0f;
+    c[j] = (v && a.c0) ? (float)a.c0[si] : 0.0f;
+    hcur[j] = (v && a.h0) ? a.h0[si] : (_Float16)0.0f;
   }
-  const int hoff = frag_index(n, u0);  // where this lane's 4 h values go (8 B, contiguous per wave)
-  *reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(hfrag[0]) + hoff) = hcur;
+  const int hoff = frag_index<ROWS>(r, uo);  // where this lane's UPL h values go (contiguous)
+  auto hist_h = [&](int slot) -> _Float16* { return reinterpret_cast<_Float16*>(hist + slot * (KCR * FV)) + hoff; };
+  *reinterpret_cast<hvec*>(hist_h(CH - 1)) = hcur;
 
   const bool has_up = layer > 0;
   const bool has_down = layer < a.L - 1;
-  const int kin = has_up ? KCI : a.kc_in0;  // input fragments per step
-  const size_t hstep = (size_t)KCR * kFrag;  // f16x8 per (tile, step) in the hand-off buffer
+  const int kin = has_up ? KCI : a.kc_in0;  // input fragment blocks per step
+  const size_t hstep = (size_t)KCR * FV;     // f16x8 per (tile, step) in the hand-off buffer
   const f16x8* in_seq = has_up ? a.hseq + ((size_t)(layer - 1) * a.ntile + tile) * a.T * hstep
-                               : a.xp + (size_t)tile * a.T * kin * kFrag;
-  _Float16* out_seq_h = has_down ? reinterpret_cast<_Float16*>(a.hseq + ((size_t)layer * a.ntile + tile) * a.T * hstep) + hoff
-                                 : nullptr;
+                               : a.xp + (size_t)tile * a.T * kin * FV;
+  f16x8* out_seq_h = has_down ? a.hseq + ((size_t)layer * a.ntile + tile) * a.T * hstep : nullptr;
   const uint32_t* up_ctr = has_up ? a.counters + (layer - 1) * a.ntile + tile : nullptr;
   uint32_t* my_ctr = a.counters + layer * a.ntile + tile;
   const int sync_tid = C::kWaves > 1 ? 64 : 0;  // the lane that polls upstream (wave 1)
@@ -180,22 +209,33 @@ lstm_wavefront_kernel(ForwardArgs a) {
   f16x8 R[RN];
   auto load_chunk = [&](int k) {
     const int s0 = k * CH;
-    const int ns = min(CH, Tt - s0);
-    const int nel = ns * kin * kFrag;
-    const f16x8* src = in_seq + (size_t)s0 * kin * kFrag;
+    const int nel = min(CH, Tt - s0) * kin * FV;
+    const f16x8* src = in_seq + (size_t)s0 * kin * FV;
 #pragma unroll
-    for (int r = 0; r < RN; ++r) {
-      const int idx = threadIdx.x + r * NT;
-      if (idx < nel) R[r] = src[idx];
+    for (int i = 0; i < RN; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < nel) R[i] = src[idx];
     }
   };
+  // The ring always holds KCI fragment blocks per step; layer 0 fills the first kin of them (the
+  // others stay zero from the initialisation), so every layer runs the same branch-free MFMAs.
   auto store_chunk = [&](int k) {
-    const int ns = min(CH, Tt - k * CH);
-    const int nel = ns * kin * kFrag;
+    const int per = kin * FV;
+    const int nel = min(CH, Tt - k * CH) * per;
 #pragma unroll
-    for (int r = 0; r < RN; ++r) {
-      const int idx = threadIdx.x + r * NT;
-      if (idx < nel) ring[idx] = R[r];
+    for (int i = 0; i < RN; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < nel) ring[(idx / per) * (KCI * FV) + idx % per] = R[i];
+    }
+  };
+  // Hand-off copy of chunk k's h history (LDS) to the global sequence buffer.
+  auto copy_out = [&](int k) {
+    const int nel = min(CH, Tt - k * CH) * (KCR * FV);
+    f16x8* dst = out_seq_h + (size_t)k * CH * hstep;
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < nel) dst[idx] = hist[idx];
     }
   };
   auto need_for = [&](int k) -> uint32_t { return (uint32_t)min((k + 1) * CH, Tt); };  // chunk k published
@@ -213,15 +253,18 @@ lstm_wavefront_kernel(ForwardArgs a) {
   auto write_probe = [&](int p) {
     if (!row_ok) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = u0 + i;
+    for (int j = 0; j < UPL; ++j) {
+      const int u = uo + j;
       if (u < a.H) {
         const size_t o = (((size_t)p * a.L + layer) * a.B + grow) * a.H + u;
-        a.probe_h[o] = (float)hcur[i];
-        a.probe_c[o] = c[i];
+        a.probe_h[o] = (float)hcur[j];
+        a.probe_c[o] = c[j];
       }
     }
   };
+
+  for (int i = threadIdx.x; i < CH * KCI * FV; i += NT) ring[i] = f16x8{};
+  __syncthreads();
 
   bool ok = true;
   uint32_t poll = 0;  // deferred observation of the upstream counter (sync_tid only)
@@ -237,14 +280,15 @@ lstm_wavefront_kernel(ForwardArgs a) {
     }
     if (has_up && threadIdx.x == sync_tid) poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();  // ring (chunk 0) and hfrag[0] visible
+  __syncthreads();  // ring (chunk 0) and the initial h visible
 
+  const bool hi = ibase != 0;
   for (int k = 0; ok && k < nchunk; ++k) {
     if (k > 0) {
-      // Chunk boundary: publish chunk k-1, move chunk k from VGPRs into the ring, acquire chunk k+1.
+      // Chunk boundary: hand chunk k-1's h to global memory, move chunk k's input from VGPRs into
+      // the ring, acquire chunk k+1 of the upstream layer and start loading it.
       __syncthreads();
-      if (has_down && threadIdx.x == 0)
-        __hip_atomic_store(my_ctr, (uint32_t)(k * CH), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      if (has_down) copy_out(k - 1);
       store_chunk(k);
       const bool more = k + 1 < nchunk;
       const int slot = wait_idx++ & 1;
@@ -260,7 +304,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
         poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_ok[slot] = okv;
       }
-      __syncthreads();
+      __syncthreads();  // also orders every wave's hand-off stores before the publication below
       if (has_up && more && s_ok[slot] == 0) {
         ok = false;
         break;
@@ -269,59 +313,85 @@ lstm_wavefront_kernel(ForwardArgs a) {
     }
 
     const int ns = min(CH, Tt - k * CH);
+    // Chunk k-1 is published halfway through chunk k: its stores have drained by then, so the
+    // release costs the publishing wave little.
+    const int pub_s = (k > 0 && has_down) ? min(CH / 2, ns - 1) : -1;
+    f32x4 acc_next[4];
+    {
+      const f16x8* xr = ring + fl;
+      f16x8 xv[KCI];
+#pragma unroll
+      for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
+#pragma unroll
+      for (int kc = 0; kc < KCI; ++kc)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
+    }
     for (int s = 0; s < ns; ++s) {
       const int t = k * CH + s;
       f32x4 acc[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = bias[q];
-      // Input part (independent of h_{t-1}).
-      const f16x8* xr = ring + s * kin * kFrag + lane;
+      for (int q = 0; q < 4; ++q) acc[q] = acc_next[q];
+      // Recurrent part: h_{t-1} from the history slot of the previous step.
+      const f16x8* hr = hist + (s == 0 ? CH - 1 : s - 1) * (KCR * FV) + fl;
+      f16x8 hv[KCR];
 #pragma unroll
-      for (int kc = 0; kc < KCI; ++kc) {
-        if (kc < kin) {
-          const f16x8 xv = xr[kc * kFrag];
+      for (int kr = 0; kr < KCR; ++kr) hv[kr] = hr[kr * FV];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv, acc[q], 0, 0, 0);
-        }
-      }
-      // Recurrent part.
-      const f16x8* hr = &hfrag[t & 1][lane];
-#pragma unroll
-      for (int kr = 0; kr < KCR; ++kr) {
-        const f16x8 hv = hr[kr * kFrag];
+      for (int kr = 0; kr < KCR; ++kr)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[KCI + kr][q], hv, acc[q], 0, 0, 0);
-      }
+          acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[KCI + kr][q], hv[kr], acc[q], 0, 0, 0);
 
-      // Gates and state update on the accumulators: lane holds units u0..u0+3 of row n.
+      // Next step's input part (the chunk's last step recomputes a discarded in-range step),
+      // interleaved with this step's gate math: each (unit, row) piece of the epilogue is preceded
+      // by its share of the next step's MFMAs and fenced with sched_barrier, so the matrix core
+      // runs while the VALU evaluates the gates (in-order issue would otherwise queue all VALU
+      // work behind the MFMAs).
+      const f16x8* xr = ring + min(s + 1, ns - 1) * (KCI * FV) + fl;
+      f16x8 xv[KCI];
+#pragma unroll
+      for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
       const bool live = t < len;
+      constexpr int kMfmaPerPiece = (KCI * 4 + UPL - 1) / UPL;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ig = sigmoid_fast(acc[0][i]);
-        const float fg = sigmoid_fast(acc[1][i]);
-        const float gg = tanh_fast(acc[2][i]);
-        const float og = sigmoid_fast(acc[3][i]);
-        const float cn = fmaf(fg, c[i], ig * gg);
-        const _Float16 hn = (_Float16)(og * tanh_fast(cn));
-        if (live) {
-          c[i] = cn;
-          hcur[i] = hn;
+      for (int j = 0; j < UPL; ++j) {
+#pragma unroll
+        for (int m = j * kMfmaPerPiece; m < (j + 1) * kMfmaPerPiece && m < KCI * 4; ++m) {
+          const int kc = m / 4, q = m % 4;
+          acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
         }
+        // this lane's pair j: D element ibase + j of every gate tile
+        const float zi = hi ? acc[0][2 + j % 2] : acc[0][j];
+        const float zf = hi ? acc[1][2 + j % 2] : acc[1][j];
+        const float zg = hi ? acc[2][2 + j % 2] : acc[2][j];
+        const float zo = hi ? acc[3][2 + j % 2] : acc[3][j];
+        float cn = c[j], hn;
+        lstm_cell(zi, zf, zg, zo, cn, hn);
+        // selects, not a branch: rows past their length keep their state
+        c[j] = live ? cn : c[j];
+        hcur[j] = live ? (_Float16)hn : hcur[j];
+        __builtin_amdgcn_sched_barrier(0);
       }
-      *reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(hfrag[(t + 1) & 1]) + hoff) = hcur;
-      if (has_down) *reinterpret_cast<f16x4*>(out_seq_h + (size_t)t * hstep * 8) = hcur;
+      *reinterpret_cast<hvec*>(hist_h(s)) = hcur;
       if (!has_down && a.out_seq && row_ok) {
-        _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + u0;
+        _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (u0 + i < a.H) dst[i] = live ? hcur[i] : (_Float16)0.0f;
+        for (int j = 0; j < UPL; ++j)
+          if (uo + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
       }
       if (t + 1 == probe_next) {
         write_probe(probe_i);
         ++probe_i;
         probe_next = probe_i < a.n_probe ? a.probe_steps[probe_i] : -1;
       }
+      if (s == pub_s && threadIdx.x == 0)
+        __hip_atomic_store(my_ctr, (uint32_t)(k * CH), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
       lds_barrier();
     }
   }
@@ -330,8 +400,8 @@ lstm_wavefront_kernel(ForwardArgs a) {
     // A hand-off wait failed (the status word records it and fails every other wait): poison this
     // tile's head outputs and leave.
     if (!has_down && a.out) {
-      for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
-        const int g = a.row0 + tile * 16 + idx / a.O;
+      for (int idx = threadIdx.x; idx < ROWS * a.O; idx += NT) {
+        const int g = a.row0 + tile * ROWS + idx / a.O;
         if (g < a.row_end) a.out[(size_t)g * a.O + idx % a.O] = (_Float16)__builtin_nanf("");
       }
     }
@@ -339,7 +409,19 @@ lstm_wavefront_kernel(ForwardArgs a) {
   }
   if (has_down && Tt > 0) {
     __syncthreads();
+    copy_out(nchunk - 1);
+    __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(my_ctr, (uint32_t)Tt, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // Steps past the tile's longest row were never visited: their output sequence is zero.
+  if (!has_down && a.out_seq && row_ok) {
+    for (int t = Tt; t < a.T; ++t) {
+      _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
+#pragma unroll
+      for (int j = 0; j < UPL; ++j)
+        if (uo + j < a.H) dst[j] = (_Float16)0.0f;
+    }
   }
 
   // States after the tile's last step (rows that ended earlier were frozen at their last step).
@@ -349,27 +431,27 @@ lstm_wavefront_kernel(ForwardArgs a) {
   }
   if (row_ok) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = u0 + i;
+    for (int j = 0; j < UPL; ++j) {
+      const int u = uo + j;
       if (u < a.H) {
         const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
-        if (a.h_n) a.h_n[si] = hcur[i];
-        if (a.c_n) a.c_n[si] = (_Float16)c[i];
+        if (a.h_n) a.h_n[si] = hcur[j];
+        if (a.c_n) a.c_n[si] = (_Float16)c[j];
       }
     }
   }
 
-  // Linear head on the final h of the last layer (written to hfrag[Tt & 1] by the last step).
+  // Linear head on the final h of the last layer (history slot of the tile's last step).
   if (!has_down && a.out) {
-    const _Float16* hf = reinterpret_cast<const _Float16*>(hfrag[Tt & 1]);
-    for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
-      const int r = idx / a.O, o = idx % a.O;
-      const int g = a.row0 + tile * 16 + r;
+    const _Float16* hf = reinterpret_cast<const _Float16*>(hist + ((Tt + CH - 1) % CH) * (KCR * FV));
+    for (int idx = threadIdx.x; idx < ROWS * a.O; idx += NT) {
+      const int rr = idx / a.O, o = idx % a.O;
+      const int g = a.row0 + tile * ROWS + rr;
       if (g >= a.row_end) continue;
       const float* wr = a.wlin + (size_t)o * HP;
       float s0 = 0.f, s1 = 0.f;
       for (int k8 = 0; k8 < HP; k8 += 8) {
-        const f16x8 hv = *reinterpret_cast<const f16x8*>(hf + frag_index(r, k8));
+        const f16x8 hv = *reinterpret_cast<const f16x8*>(hf + frag_index<ROWS>(rr, k8));
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
           s0 = fmaf((float)hv[j], wr[k8 + j], s0);
@@ -389,7 +471,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
 template <int HP>
 __global__ void pack_layer_kernel(const _Float16* __restrict__ w_ih, const _Float16* __restrict__ w_hh, int K,
                                   int H, _Float16* __restrict__ dst) {
-  using C = Tile<HP>;
+  using C = Tile<HP, 16, 1>;
   const size_t total = (size_t)C::kWaves * C::kKc * 4 * 64 * 8;
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= total) return;
@@ -437,19 +519,21 @@ __global__ void pack_linear_kernel(const _Float16* __restrict__ w, const _Float1
   if (e < O) bl[e] = b ? (float)b[e] : 0.0f;
 }
 
-// x [B, T, I] -> xp [ntile][T][kci0][64 lanes] f16x8 in B-fragment order, zero padded.
+// x [B, T, I] -> xp [ntile][T][kci0][4][rows] f16x8: B-fragment order for tiles of `rows` rows,
+// zero padded.
 __global__ void pack_x_kernel(const _Float16* __restrict__ x, int T, int I, int row0, int row_end, int ntile,
-                              int kci0, f16x8* __restrict__ xp) {
+                              int rows, int kci0, f16x8* __restrict__ xp) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const size_t total = (size_t)ntile * T * kci0 * kFrag;
+  const int fv = 4 * rows;
+  const size_t total = (size_t)ntile * T * kci0 * fv;
   if (e >= total) return;
-  const int lane = (int)(e % kFrag);
-  const int kc = (int)((e / kFrag) % kci0);
-  const size_t tt = e / ((size_t)kFrag * kci0);
+  const int f = (int)(e % fv);
+  const int kc = (int)((e / fv) % kci0);
+  const size_t tt = e / ((size_t)fv * kci0);
   const int t = (int)(tt % T);
   const int tile = (int)(tt / T);
-  const int b = row0 + tile * 16 + (lane & 15);
-  const int k0 = kc * 32 + (lane >> 4) * 8;
+  const int b = row0 + tile * rows + f % rows;
+  const int k0 = kc * 32 + (f / rows) * 8;
   f16x8 v = {};
   if (b < row_end) {
     const _Float16* src = x + ((size_t)b * T + t) * I;
@@ -526,11 +610,12 @@ PackedLayout packed_layout(const Geometry& g) {
   return p;
 }
 
-WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows) {
+WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows, int tile_rows) {
   WorkspaceLayout w;
-  const size_t ntile = (size_t)chunk_rows / 16;
-  const size_t frag_bytes = (size_t)kFrag * 16;  // one 16 x 32 fp16 fragment block
+  const size_t ntile = (size_t)chunk_rows / tile_rows;
+  const size_t frag_bytes = (size_t)4 * tile_rows * 16;  // one [tile_rows x 32] fp16 fragment block
   w.chunk_rows = chunk_rows;
+  w.tile_rows = tile_rows;
   w.status = 0;
   w.counters = 256;
   w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile);
@@ -570,10 +655,10 @@ hipError_t launch_pack_linear(const Geometry& g, const _Float16* w, const _Float
 }
 
 hipError_t launch_pack_x(const Geometry& g, const ForwardArgs& a, hipStream_t s) {
-  const size_t n = (size_t)a.ntile * a.T * g.kc_in0 * kFrag;
+  const size_t n = (size_t)a.ntile * a.T * g.kc_in0 * 4 * a.tile_rows;
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(pack_x_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, a.I, a.row0, a.row_end, a.ntile, g.kc_in0,
-                     a.xp);
+  hipLaunchKernelGGL(pack_x_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, a.I, a.row0, a.row_end, a.ntile,
+                     a.tile_rows, g.kc_in0, a.xp);
   return hipGetLastError();
 }
 
@@ -596,17 +681,22 @@ hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, 
 #endif
 constexpr int kChunk = PLH_CHUNK_STEPS;
 
-static const void* recurrent_kernel(const Geometry& g) {
-  switch (g.HP) {
-    case 32: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<32, kChunk>);
-    case 64: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<64, kChunk>);
-    case 128: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<128, kChunk>);
+template <int ROWS>
+static const void* recurrent_kernel_rows(int HP) {
+  switch (HP) {
+    case 32: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<32, ROWS, kChunk>);
+    case 64: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<64, ROWS, kChunk>);
+    case 128: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<128, ROWS, kChunk>);
     default: return nullptr;
   }
 }
 
-int recurrent_capacity(const Geometry& g, hipError_t* err) {
-  const void* fn = recurrent_kernel(g);
+static const void* recurrent_kernel(const Geometry& g, int tile_rows) {
+  return tile_rows == 8 ? recurrent_kernel_rows<8>(g.HP) : tile_rows == 16 ? recurrent_kernel_rows<16>(g.HP) : nullptr;
+}
+
+int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err) {
+  const void* fn = recurrent_kernel(g, tile_rows);
   if (!fn) {
     *err = hipErrorInvalidValue;
     return 0;
@@ -620,7 +710,7 @@ int recurrent_capacity(const Geometry& g, hipError_t* err) {
 }
 
 hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s) {
-  const void* fn = recurrent_kernel(g);
+  const void* fn = recurrent_kernel(g, a.tile_rows);
   if (!fn) return hipErrorInvalidValue;
   ForwardArgs args = a;
   void* params[] = {&args};

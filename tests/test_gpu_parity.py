@@ -204,3 +204,20 @@ def test_reference_extension_surface(gpu):
     assert_close(a.float().cpu().numpy(), want.float().cpu().numpy(), max_abs=2e-3, mean_abs=5e-4, what="generic")
     assert torch.equal(a, b)
     assert torch.equal(r, a[:1].expand(7, -1))
+
+
+@pytest.mark.parametrize("B,T", [(600, 120), (2100, 40)])
+def test_large_batches_use_16_row_tiles_and_split_launches(gpu, B, T):
+    """600 rows need 16-row tiles to fit one co-resident launch; 2100 rows need several launches."""
+    I, H, L, O = 5, 128, 4, 24
+    _say(f"large batch B={B} T={T}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    model = _gpu_model(native)
+    got = model(x.to("cuda", torch.float16))
+    gpu.check_status(torch.device("cuda"))
+    want = _torch_ref(native, x)
+    assert_close(got.float().cpu().numpy(), want, what=f"B={B}")
+    rows = np.r_[0:8, B // 2:B // 2 + 8, B - 8:B]
+    ref = oracle.regressor_forward(x.numpy()[rows], oracle_layers(native.lstm), *linear_params(native.linear))
+    assert_close(got.float().cpu().numpy()[rows], ref, what=f"B={B} vs oracle")

@@ -36,6 +36,7 @@ METRIC = "fwd latency (s) + seq-steps/s, L4 H128 b512 s1000 fp16; MFMA util %"
 I, H, L, O, B, T = 5, 128, 4, 24, 512, 1000
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA peak (no sparsity)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "lstm_wavefront_c2_traffic.txt")
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "lstm_wavefront_c2_counters.txt")
 
 
 def algorithmic_flops(I, H, L, O, B, T) -> float:
@@ -43,16 +44,21 @@ def algorithmic_flops(I, H, L, O, B, T) -> float:
     return 2.0 * B * T * 4 * H * ((I + H) + (L - 1) * 2 * H) + 2.0 * B * H * O
 
 
-def read_traffic():
-    """HBM bytes per launch of the persistent kernel from the committed rocprofv3 PMC summary."""
+def _profile_value(path, key):
+    """A `key: value` line of a committed rocprofv3 summary under profiles/, or None."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
-    except OSError:
+                if line.startswith(key + ":"):
+                    return float(line.split(":", 1)[1].split("#")[0])
+    except (OSError, ValueError):
         pass
     return None
+
+
+def read_traffic():
+    """HBM bytes per launch of the persistent kernel (FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
+    return _profile_value(TRAFFIC_FILE, "traffic_bytes_per_launch")
 
 
 def cpu_model_name() -> str:
@@ -188,12 +194,12 @@ def main() -> int:
                         "(seed 42), h0=c0=0",
             "global_batch": B,
             "seq_len": T,
-            "parallelism": "single GPU: persistent layer-wavefront grid (layers x 16-row batch tiles)",
+            "parallelism": "single GPU: persistent layer-wavefront grid (4 layers x 64 tiles of 8 batch rows)",
         },
         "latency_s": median_ms * 1e-3,
         "latency_100_fwd_wall_s": wall * 100.0 / args.steps,
         "kernel": {
-            "name": "lstm_wavefront_kernel<128,8>",
+            "name": "lstm_wavefront_kernel<128,8,8>",
             "avg_ms": kernel_ms,
             "per_step_us": kernel_ms * 1e3 / (T + L - 1),
             "timed_launches": n_timed,
@@ -206,6 +212,12 @@ def main() -> int:
             "frac": achieved / PEAK_FP16_TFLOPS,
             "traffic": read_traffic(),
             "flops_per_launch": flops,
+        },
+        "mfma_util": {
+            "algorithmic_percent": 100.0 * achieved / PEAK_FP16_TFLOPS,
+            "rocprof_busy_percent": _profile_value(COUNTERS_FILE, "MfmaUtil_percent"),
+            "lds_bank_conflict_percent": _profile_value(COUNTERS_FILE, "LDSBankConflict_percent"),
+            "source": "profiles/lstm_wavefront_c2_counters.txt (rocprofv3 --pmc on the same kernel and shape)",
         },
         "reference_published": {
             "fwd_100_s": 3.08,

@@ -7,7 +7,10 @@
 // depend on them.
 //
 //   plh_bench [--input 5] [--hidden 128] [--layers 4] [--output 24] [--batch 512] [--seq 1000]
-//             [--warmup 10] [--iters 100] [--ragged MIN]
+//             [--warmup 10] [--iters 100] [--ragged MIN] [--copy-mb N]
+//
+// --copy-mb N ends the run with three device-to-device copies of N MiB: a plain copy kernel of
+// known size, whose memory counters calibrate the forward's HBM traffic in a profiler.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -85,6 +88,7 @@ int main(int argc, char** argv) {
   const int B = arg_int(argc, argv, "--batch", 512), T = arg_int(argc, argv, "--seq", 1000);
   const int warmup = arg_int(argc, argv, "--warmup", 10), iters = arg_int(argc, argv, "--iters", 100);
   const int ragged_min = arg_int(argc, argv, "--ragged", 0);
+  const int copy_mb = arg_int(argc, argv, "--copy-mb", 0);
   if (!plh_supports(I, H, L, O)) {
     std::fprintf(stderr, "unsupported geometry: %s\n", plh_last_error());
     return 1;
@@ -155,6 +159,17 @@ int main(int argc, char** argv) {
   HIP_OK(hipMemcpy(host_out.data(), out, host_out.size() * 2, hipMemcpyDeviceToHost));
   double checksum = 0.0;
   for (auto v : host_out) checksum += std::fabs((double)v);
+  if (copy_mb > 0) {
+    void *src = nullptr, *dst = nullptr;
+    const size_t bytes = (size_t)copy_mb << 20;
+    HIP_OK(hipMalloc(&src, bytes));
+    HIP_OK(hipMalloc(&dst, bytes));
+    HIP_OK(hipMemsetAsync(src, 1, bytes, s));
+    for (int i = 0; i < 3; ++i) HIP_OK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s));
+    HIP_OK(hipStreamSynchronize(s));
+    HIP_OK(hipFree(src));
+    HIP_OK(hipFree(dst));
+  }
   const double fwd_ms = total_ms / iters, kern_ms = kernel_ms / std::max(timed, 1);
   std::printf(
       "{\"geometry\": [%d, %d, %d, %d], \"batch\": %d, \"seq\": %d, \"iters\": %d, \"fwd_ms\": %.6f, "

@@ -51,9 +51,10 @@ int capacity(const plh::Geometry& g, int tile_rows, hipError_t* err) {
   return c;
 }
 
-// Launch plan: every (layer, tile) workgroup of one persistent launch must be co-resident.
+// Launch plan: every (layer, tile, slice) workgroup of one persistent launch must be co-resident.
 // 8-row tiles halve the gate math per workgroup and are used when the whole batch fits one launch
 // with them; otherwise 16-row tiles, and the batch is split into sequential launches if needed.
+// Sliced geometries (HP 256, 512) always use 16-row tiles.
 struct Plan {
   int tile_rows = 16;
   int chunk_rows = 16;
@@ -63,12 +64,12 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
   Plan p;
   batch = std::max(batch, 1);
   const int tiles8 = (batch + 7) / 8;
-  if ((long long)g.L * tiles8 <= cap8) {
+  if (g.slices == 1 && (long long)g.L * tiles8 <= cap8) {
     p.tile_rows = 8;
     p.chunk_rows = tiles8 * 8;
     return p;
   }
-  int tiles = cap16 / g.L;
+  int tiles = cap16 / (g.L * g.slices);
   if (tiles >= 8) tiles &= ~7;  // keep the XCD-aware mapping available
   tiles = std::max(1, std::min(tiles, (batch + 15) / 16));
   p.tile_rows = 16;
@@ -79,7 +80,7 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
 // Plan on the current device; without one (capacity unknown) assume one workgroup per CU of a
 // 256-CU MI355X.
 Plan plan_for(const plh::Geometry& g, int batch, bool need_device, hipError_t* err) {
-  int cap8 = capacity(g, 8, err);
+  int cap8 = g.slices == 1 ? capacity(g, 8, err) : 0;
   int cap16 = *err == hipSuccess ? capacity(g, 16, err) : 0;
   if (*err != hipSuccess) {
     if (need_device) return Plan();
@@ -198,8 +199,9 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   hipError_t err = hipSuccess;
   const Plan plan = plan_for(g, batch, true, &err);
   if (err != hipSuccess) return fail_hip(err, "occupancy query");
-  if (capacity(g, 16, &err) < g.L)
-    return fail(PLH_ERR_UNSUPPORTED, "the device cannot hold one workgroup per layer co-resident (layers = " +
+  if (capacity(g, 16, &err) < g.L * g.slices)
+    return fail(PLH_ERR_UNSUPPORTED, "the device cannot hold the " + std::to_string(g.L * g.slices) +
+                                         " workgroups of one batch tile co-resident (layers = " +
                                          std::to_string(g.L) + ")");
   const int chunk_rows = plan.chunk_rows;
   const plh::WorkspaceLayout w = plh::workspace_layout(g, seq_len, chunk_rows, plan.tile_rows);
@@ -254,7 +256,7 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     a.tile_rows = plan.tile_rows;
     a.ntile = (rows + plan.tile_rows - 1) / plan.tile_rows;
     a.rows_pad = a.ntile * plan.tile_rows;
-    a.xcd_map = (a.ntile % 8 == 0) ? 1 : 0;
+    a.xcd_map = (g.slices > 1 ? (g.L * a.ntile) % 8 : a.ntile % 8) == 0 ? 1 : 0;
     err = plh::launch_zero_u32(counters, (size_t)g.L * a.ntile, s);
     if (err != hipSuccess) return fail_hip(err, "counter reset");
     err = plh::launch_pack_x(g, a, s);

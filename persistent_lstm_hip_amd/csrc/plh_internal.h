@@ -16,10 +16,11 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 // i = f = o = 0.5, g = 0 and their c and h stay exactly 0: padding never changes real outputs.
 struct Geometry {
   int I, H, L, O;
-  int HP;      // padded hidden size: 32, 64 or 128
-  int waves;   // HP / 16: one wave per 16 hidden units (its i, f, g, o gate columns)
+  int HP;      // padded hidden size: 32, 64, 128 (one workgroup per layer and tile) or 256, 512 (sliced)
+  int slices;  // workgroups per (layer, tile): 1, or HP / 64 (HP = 256) and HP / 32 (HP = 512)
+  int waves;   // waves per workgroup: HP / 16 (one per 16 hidden units) or 8 when sliced
   int kci;     // input-part K chunks of 32 for layers >= 1 (= HP / 32)
-  int kc;      // K chunks per wave: input part + recurrent part (= 2 * kci)
+  int kc;      // K chunks of [W_ih | W_hh] per gate row (= 2 * kci)
   int kc_in0;  // input-part K chunks layer 0 uses (= ceil(I / 32) <= kci)
 };
 
@@ -28,7 +29,8 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why);
 
 // Byte offsets of the packed-weight blob (all 256-byte aligned).
 struct PackedLayout {
-  size_t wpack;  // f16 [L][waves][kc][4 gates][64 lanes][8]: each lane's MFMA A fragments
+  size_t wpack;  // f16 MFMA A fragments of every lane: [L][waves][kc][4 gates][64 lanes][8], or when
+                 // sliced [L][slices][8 waves][8 chunks][4 gates][64 lanes][8]
   size_t bias;   // f32 [L][4][HP]: b_ih + b_hh
   size_t wlin;   // f32 [O][HP]
   size_t blin;   // f32 [O]
@@ -40,7 +42,8 @@ PackedLayout packed_layout(const Geometry& g);
 //   status   u32                                   PLH_STATUS_* bits
 //   counters u32 [L][ntile]                        steps published per (layer, tile)
 //   xp       f16x8 [ntile][T][kc_in0][4][R]        x in B-fragment order (layer 0 input)
-//   hseq     f16x8 [L-1][ntile][T][kci][4][R]      h of layers 0..L-2 in B-fragment order
+//   hseq     f16x8 [L'][ntile][T][kci][4][R]       h of layers 0..L'-1 in B-fragment order; L' = L-1,
+//                                                  or L when sliced (slices exchange h_t through it)
 struct WorkspaceLayout {
   size_t status, counters, xp, hseq, total;
   int chunk_rows;  // batch rows per persistent launch (co-residency bound), multiple of tile_rows

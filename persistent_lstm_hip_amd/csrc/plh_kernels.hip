@@ -464,6 +464,348 @@ lstm_wavefront_kernel(ForwardArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Hidden sizes above 128.  A layer's [W_ih | W_hh] (1 MB at H = 256, 4 MB at H = 512) no longer fits
+// one CU's register file, so each (layer, 16-row tile) is served by S workgroups ("slices"), each
+// keeping the gate rows of HS = HP / S hidden units resident in VGPRs:
+//   * the 8 waves of a slice form HS/16 unit groups; within a group, KSP waves hold the input part
+//     (W_ih columns, 256 per wave) and KSP waves the recurrent part (W_hh columns), so every wave's
+//     resident weights are 8 K-chunks x 4 gates = 128 VGPRs;
+//   * per step each wave computes its partial gate sums with MFMA, the partials meet in LDS, and
+//     the group's waves split the gate math of its 16 units x 16 rows;
+//   * h_t of the slice goes to the hand-off buffer; the S slices count steps on one shared counter
+//     (agent-scope release add / acquire) and every slice reloads the full h_t from global memory
+//     for its next recurrent part.  The same counter drives the chunked hand-off to the next layer,
+//     so layers still run as a wavefront.
+template <int HP>
+struct Sliced {
+  static constexpr int kKsp = HP / 256;     // waves per K part of a unit group
+  static constexpr int kGroups = 4 / kKsp;  // 16-unit groups per workgroup
+  static constexpr int kHs = 16 * kGroups;  // hidden units per workgroup
+  static constexpr int kS = HP / kHs;       // workgroups per (layer, tile)
+  static constexpr int kKch = HP / 32;      // K chunks of one part
+  static constexpr int kWpg = 2 * kKsp;     // waves per unit group
+  static constexpr int kUpw = 4 / kWpg;     // D rows (units) of a lane that each wave of the group evaluates
+};
+
+// Workgroup -> (layer, tile, slice).  With xcd_map the S slices of a (layer, tile) share an XCD.
+__device__ __forceinline__ void sliced_coords(int b, int L, int ntile, int S, int xcd_map, int& layer, int& tile,
+                                              int& slice) {
+  int grp;
+  if (xcd_map) {
+    const int j = b >> 3;
+    slice = j % S;
+    grp = (j / S) * 8 + (b & 7);
+  } else {
+    slice = b % S;
+    grp = b / S;
+  }
+  layer = grp / ntile;
+  tile = grp % ntile;
+  (void)L;
+}
+
+template <int HP, int CH>
+__global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
+  using C = Sliced<HP>;
+  constexpr int KSP = C::kKsp, HS = C::kHs, S = C::kS, KCH = C::kKch, WPG = C::kWpg, UPW = C::kUpw;
+  constexpr int NT = 512, FV = 64;  // 16-row fragment blocks
+  constexpr int RN = (CH * KCH * FV + NT - 1) / NT;
+  constexpr int KCW = 8;            // K chunks per wave
+
+  __shared__ f16x8 ring[CH * KCH * FV];  // step inputs of the current chunk (all HP input units)
+  __shared__ f16x8 hbuf[KCH * FV];       // h_{t-1} of all HP units
+  __shared__ f32x4 part[8][4][64];       // partial gate sums of every wave
+  __shared__ int s_ok[2];
+  __shared__ int s_tlen;
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  int layer, tile, slice;
+  sliced_coords(blockIdx.x, a.L, a.ntile, S, a.xcd_map, layer, tile, slice);
+  const int g = wave / WPG, ew = wave % WPG;
+  const bool recurrent = ew >= KSP;  // this wave holds W_hh columns
+  const int kq = ew % KSP;           // which 256-column quarter of its part
+
+  const int grow = a.row0 + tile * 16 + n;
+  const bool row_ok = grow < a.row_end;
+  int len = 0;
+  if (row_ok) {
+    len = a.lengths ? a.lengths[grow] : a.T;
+    len = len < 0 ? 0 : (len > a.T ? a.T : len);
+  }
+  if (threadIdx.x == 0) s_tlen = 0;
+  __syncthreads();
+  if (wave == 0 && kg == 0) atomicMax(&s_tlen, len);
+  __syncthreads();
+  const int Tt = s_tlen;
+
+  f16x8 w[KCW][4];
+  {
+    const f16x8* wp = reinterpret_cast<const f16x8*>(a.wpack) +
+                      ((size_t)((layer * S + slice) * 8 + wave) * KCW * 4) * 64 + lane;
+#pragma unroll
+    for (int kc = 0; kc < KCW; ++kc)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
+  }
+  const int u0 = slice * HS + g * 16 + kg * 4;  // units of this lane's 4 D rows
+  const int uo = u0 + ew * UPW;                 // the UPW of them this wave evaluates
+  float bq[4][UPW];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int j = 0; j < UPW; ++j) bq[q][j] = a.bias[((size_t)layer * 4 + q) * HP + uo + j];
+
+  float c[UPW];
+  _Float16 hcur[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; ++j) {
+    const int u = uo + j;
+    const bool v = row_ok && u < a.H;
+    const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
+    c[j] = (v && a.c0) ? (float)a.c0[si] : 0.0f;
+    hcur[j] = (v && a.h0) ? a.h0[si] : (_Float16)0.0f;
+  }
+  // h_{-1} of all units into hbuf (fragment order)
+  for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) {
+    const int kc = idx / FV, l = idx % FV;
+    const int gr = a.row0 + tile * 16 + (l & 15);
+    const int k0 = kc * 32 + (l >> 4) * 8;
+    f16x8 v = {};
+    if (a.h0 && gr < a.row_end) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (k0 + j < a.H) v[j] = a.h0[((size_t)layer * a.B + gr) * a.H + k0 + j];
+    }
+    hbuf[idx] = v;
+  }
+
+  const bool has_up = layer > 0;
+  const int kin = has_up ? KCH : a.kc_in0;
+  const size_t hstep = (size_t)KCH * FV;
+  const f16x8* in_seq = has_up ? a.hseq + ((size_t)(layer - 1) * a.ntile + tile) * a.T * hstep
+                               : a.xp + (size_t)tile * a.T * kin * FV;
+  f16x8* my_seq = a.hseq + ((size_t)layer * a.ntile + tile) * a.T * hstep;
+  _Float16* my_seq_h = reinterpret_cast<_Float16*>(my_seq) + ((uo >> 3) * 16 + n) * 8 + (uo & 7);
+  const uint32_t* up_ctr = has_up ? a.counters + (layer - 1) * a.ntile + tile : nullptr;
+  uint32_t* my_ctr = a.counters + layer * a.ntile + tile;
+  const int sync_tid = 64;
+
+  const int nchunk = (Tt + CH - 1) / CH;
+  f16x8 R[RN];
+  auto load_chunk = [&](int k) {
+    const int s0 = k * CH;
+    const int nel = min(CH, Tt - s0) * kin * FV;
+    const f16x8* src = in_seq + (size_t)s0 * kin * FV;
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < nel) R[i] = src[idx];
+    }
+  };
+  auto store_chunk = [&](int k) {
+    const int per = kin * FV;
+    const int nel = min(CH, Tt - k * CH) * per;
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < nel) ring[(idx / per) * (KCH * FV) + idx % per] = R[i];
+    }
+  };
+  auto need_up = [&](int k) -> uint32_t { return (uint32_t)(S * min((k + 1) * CH, Tt)); };
+
+  int wait_idx = 0;
+  auto wait_ctr = [&](const uint32_t* ctr, uint32_t need) -> bool {
+    const int slot = wait_idx++ & 1;
+    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(ctr, need, a.status);
+    __syncthreads();
+    return s_ok[slot] != 0;
+  };
+
+  int probe_i = 0;
+  int probe_next = a.n_probe > 0 ? a.probe_steps[0] : -1;
+  auto write_probe = [&](int pi) {
+    if (!row_ok) return;
+#pragma unroll
+    for (int j = 0; j < UPW; ++j) {
+      const int u = uo + j;
+      if (u < a.H) {
+        const size_t o = (((size_t)pi * a.L + layer) * a.B + grow) * a.H + u;
+        a.probe_h[o] = (float)hcur[j];
+        a.probe_c[o] = c[j];
+      }
+    }
+  };
+
+  for (int i = threadIdx.x; i < CH * KCH * FV; i += NT) ring[i] = f16x8{};
+  __syncthreads();
+
+  bool ok = true;
+  uint32_t poll = 0;
+  if (Tt > 0) {
+    if (has_up) ok = wait_ctr(up_ctr, need_up(0));
+    if (ok) {
+      load_chunk(0);
+      store_chunk(0);
+    }
+    if (ok && nchunk > 1) {
+      if (has_up) ok = wait_ctr(up_ctr, need_up(1));
+      if (ok) load_chunk(1);
+    }
+    if (has_up && threadIdx.x == sync_tid) poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+
+  for (int k = 0; ok && k < nchunk; ++k) {
+    if (k > 0) {
+      __syncthreads();
+      store_chunk(k);
+      const bool more = k + 1 < nchunk;
+      const int slot = wait_idx++ & 1;
+      if (has_up && more && threadIdx.x == sync_tid) {
+        const uint32_t need = need_up(k + 1);
+        int okv;
+        if (poll >= need) {
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          okv = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
+        } else {
+          okv = wait_counter(up_ctr, need, a.status);
+        }
+        poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_ok[slot] = okv;
+      }
+      __syncthreads();
+      if (has_up && more && s_ok[slot] == 0) {
+        ok = false;
+        break;
+      }
+      if (more) load_chunk(k + 1);
+    }
+    const int ns = min(CH, Tt - k * CH);
+    for (int s = 0; s < ns && ok; ++s) {
+      const int t = k * CH + s;
+      // Partial gate sums of this wave's K part.
+      const f16x8* src = (recurrent ? hbuf : ring + s * (KCH * FV)) + kq * KCW * FV + lane;
+      f32x4 acc[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < KCW; ++kc) {
+        const f16x8 bv = src[kc * FV];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], bv, acc[q], 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) part[wave][q][lane] = acc[q];
+      lds_barrier();
+
+      // Gate math of this wave's UPW units: sum the group's partials and the bias.
+      const bool live = t < len;
+#pragma unroll
+      for (int j = 0; j < UPW; ++j) {
+        const int i = ew * UPW + j;
+        float z[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float sum = bq[q][j];
+#pragma unroll
+          for (int e = 0; e < WPG; ++e) sum += part[g * WPG + e][q][lane][i];
+          z[q] = sum;
+        }
+        float cn = c[j], hn;
+        lstm_cell(z[0], z[1], z[2], z[3], cn, hn);
+        c[j] = live ? cn : c[j];
+        hcur[j] = live ? (_Float16)hn : hcur[j];
+      }
+      {
+        _Float16* dst = my_seq_h + (size_t)t * hstep * 8;
+#pragma unroll
+        for (int j = 0; j < UPW; ++j) dst[j] = hcur[j];
+      }
+      if (layer == a.L - 1 && a.out_seq && row_ok) {
+        _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
+#pragma unroll
+        for (int j = 0; j < UPW; ++j)
+          if (uo + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
+      }
+      if (t + 1 == probe_next) {
+        write_probe(probe_i);
+        ++probe_i;
+        probe_next = probe_i < a.n_probe ? a.probe_steps[probe_i] : -1;
+      }
+      // Publish this slice's h_t, then wait for every slice's h_t and reload the full h.
+      __syncthreads();
+      if (threadIdx.x == 0) __hip_atomic_fetch_add(my_ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      if (!wait_ctr(my_ctr, (uint32_t)(S * (t + 1)))) {
+        ok = false;
+        break;
+      }
+      {
+        const f16x8* hsrc = my_seq + (size_t)t * hstep;
+        for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) hbuf[idx] = hsrc[idx];
+      }
+      lds_barrier();
+    }
+  }
+
+  if (!ok) {
+    if (layer == a.L - 1 && slice == 0 && a.out) {
+      for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
+        const int gr = a.row0 + tile * 16 + idx / a.O;
+        if (gr < a.row_end) a.out[(size_t)gr * a.O + idx % a.O] = (_Float16)__builtin_nanf("");
+      }
+    }
+    return;
+  }
+
+  if (layer == a.L - 1 && a.out_seq && row_ok) {
+    for (int t = Tt; t < a.T; ++t) {
+      _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
+#pragma unroll
+      for (int j = 0; j < UPW; ++j)
+        if (uo + j < a.H) dst[j] = (_Float16)0.0f;
+    }
+  }
+  while (probe_i < a.n_probe) {
+    write_probe(probe_i);
+    ++probe_i;
+  }
+  if (row_ok) {
+#pragma unroll
+    for (int j = 0; j < UPW; ++j) {
+      const int u = uo + j;
+      if (u < a.H) {
+        const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
+        if (a.h_n) a.h_n[si] = hcur[j];
+        if (a.c_n) a.c_n[si] = (_Float16)c[j];
+      }
+    }
+  }
+  // Linear head (last layer, first slice) on the full final h held in hbuf.
+  if (layer == a.L - 1 && slice == 0 && a.out) {
+    const _Float16* hf = reinterpret_cast<const _Float16*>(hbuf);
+    for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
+      const int rr = idx / a.O, o = idx % a.O;
+      const int gr = a.row0 + tile * 16 + rr;
+      if (gr >= a.row_end) continue;
+      const float* wr = a.wlin + (size_t)o * HP;
+      float s0 = 0.f, s1 = 0.f;
+      for (int k8 = 0; k8 < HP; k8 += 8) {
+        const f16x8 hv = *reinterpret_cast<const f16x8*>(hf + frag_index<16>(rr, k8));
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          s0 = fmaf((float)hv[j], wr[k8 + j], s0);
+          s1 = fmaf((float)hv[j + 1], wr[k8 + j + 1], s1);
+        }
+      }
+      a.out[(size_t)gr * a.O + o] = (_Float16)(a.blin[o] + (s0 + s1));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Weight packing: torch layout -> per-lane MFMA A fragments.
 // For 16x16x32 f16, lane l of the A operand holds A[m = l % 16][k = 8 * (l / 16) + j], j < 8.
 // Row m of tile (wave w, gate q) is gate column q*H + w*16 + m; K runs over [x | h] in chunks
@@ -490,6 +832,38 @@ __global__ void pack_layer_kernel(const _Float16* __restrict__ w_ih, const _Floa
       if (k < K) v = w_ih[col * K + k];
     } else {
       const int k = (kc - C::kKci) * 32 + kgrp * 8 + j;
+      if (k < H) v = w_hh[col * H + k];
+    }
+  }
+  dst[e] = v;
+}
+
+// Sliced weights: [L][S][8 waves][8 chunks][4 gates][64 lanes][8].  Wave w of slice s holds unit
+// group g = w / WPG, part ew / KSP (0: W_ih, 1: W_hh), quarter ew % KSP of that part's columns.
+template <int HP>
+__global__ void pack_sliced_kernel(const _Float16* __restrict__ w_ih, const _Float16* __restrict__ w_hh, int K,
+                                   int H, _Float16* __restrict__ dst) {
+  using C = Sliced<HP>;
+  const size_t total = (size_t)C::kS * 8 * 8 * 4 * 64 * 8;
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= total) return;
+  const int j = e & 7;
+  const int lane = (e >> 3) & 63;
+  const int q = (e >> 9) & 3;
+  const int kc = (int)((e >> 11) & 7);
+  const int wv = (int)((e >> 14) & 7);
+  const int sl = (int)(e >> 17);
+  const int g = wv / C::kWpg, ew = wv % C::kWpg;
+  const bool rec = ew >= C::kKsp;
+  const int kq = ew % C::kKsp;
+  const int u = sl * C::kHs + g * 16 + (lane & 15);
+  const size_t col = (size_t)q * H + u;
+  const int k = (kq * 8 + kc) * 32 + (lane >> 4) * 8 + j;
+  _Float16 v = (_Float16)0.0f;
+  if (u < H) {
+    if (!rec) {
+      if (k < K) v = w_ih[col * K + k];
+    } else {
       if (k < H) v = w_hh[col * H + k];
     }
   }
@@ -569,8 +943,10 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
   if (H <= 32) HP = 32;
   else if (H <= 64) HP = 64;
   else if (H <= 128) HP = 128;
+  else if (H <= 256) HP = 256;
+  else if (H <= 512) HP = 512;
   if (HP == 0) {
-    *why = "hidden_size > 128 is not implemented by the persistent kernel";
+    *why = "hidden_size > 512 is not implemented by the persistent kernels";
     return false;
   }
   if (I > HP) {
@@ -586,7 +962,8 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
   g->L = L;
   g->O = O;
   g->HP = HP;
-  g->waves = HP / 16;
+  g->slices = HP == 256 ? Sliced<256>::kS : HP == 512 ? Sliced<512>::kS : 1;
+  g->waves = g->slices > 1 ? 8 : HP / 16;
   g->kci = HP / 32;
   g->kc = 2 * g->kci;
   g->kc_in0 = (I + 31) / 32;
@@ -599,7 +976,9 @@ PackedLayout packed_layout(const Geometry& g) {
   PackedLayout p;
   size_t off = 0;
   p.wpack = off;
-  off = align256(off + (size_t)g.L * g.waves * g.kc * 4 * 64 * 8 * sizeof(_Float16));
+  // HP / 16 gate-row groups x kc chunks of 64 lanes x 8 halfs per gate: the same size whether one
+  // workgroup or `slices` workgroups hold a layer.
+  off = align256(off + (size_t)g.L * (g.HP / 16) * g.kc * 4 * 64 * 8 * sizeof(_Float16));
   p.bias = off;
   off = align256(off + (size_t)g.L * 4 * g.HP * sizeof(float));
   p.wlin = off;
@@ -620,13 +999,14 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   w.counters = 256;
   w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile);
   w.hseq = align256(w.xp + ntile * seq_len * g.kc_in0 * frag_bytes);
-  w.total = align256(w.hseq + (size_t)(g.L - 1) * ntile * seq_len * g.kci * frag_bytes);
+  const size_t hseq_layers = g.slices > 1 ? g.L : g.L - 1;
+  w.total = align256(w.hseq + hseq_layers * ntile * seq_len * g.kci * frag_bytes);
   return w;
 }
 
 hipError_t launch_pack_layer(const Geometry& g, int layer, const _Float16* w_ih, const _Float16* w_hh, _Float16* wpack,
                              hipStream_t s) {
-  const size_t per_layer = (size_t)g.waves * g.kc * 4 * 64 * 8;
+  const size_t per_layer = (size_t)(g.HP / 16) * g.kc * 4 * 64 * 8;
   _Float16* dst = wpack + per_layer * layer;
   const int K = layer == 0 ? g.I : g.H;
   const unsigned grid = blocks_for(per_layer, 256);
@@ -634,6 +1014,8 @@ hipError_t launch_pack_layer(const Geometry& g, int layer, const _Float16* w_ih,
     case 32: hipLaunchKernelGGL(pack_layer_kernel<32>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
     case 64: hipLaunchKernelGGL(pack_layer_kernel<64>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
     case 128: hipLaunchKernelGGL(pack_layer_kernel<128>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
+    case 256: hipLaunchKernelGGL(pack_sliced_kernel<256>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
+    case 512: hipLaunchKernelGGL(pack_sliced_kernel<512>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -691,7 +1073,19 @@ static const void* recurrent_kernel_rows(int HP) {
   }
 }
 
+// Steps per hand-off chunk of the sliced kernels: the input ring holds CH * HP / 32 fragment blocks.
+constexpr int kChunk256 = 4;
+constexpr int kChunk512 = 2;
+
 static const void* recurrent_kernel(const Geometry& g, int tile_rows) {
+  if (g.slices > 1) {
+    if (tile_rows != 16) return nullptr;
+    switch (g.HP) {
+      case 256: return reinterpret_cast<const void*>(&lstm_sliced_kernel<256, kChunk256>);
+      case 512: return reinterpret_cast<const void*>(&lstm_sliced_kernel<512, kChunk512>);
+      default: return nullptr;
+    }
+  }
   return tile_rows == 8 ? recurrent_kernel_rows<8>(g.HP) : tile_rows == 16 ? recurrent_kernel_rows<16>(g.HP) : nullptr;
 }
 
@@ -714,7 +1108,7 @@ hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t
   if (!fn) return hipErrorInvalidValue;
   ForwardArgs args = a;
   void* params[] = {&args};
-  return hipLaunchCooperativeKernel(fn, dim3(a.L * a.ntile), dim3(g.waves * 64), params, 0, s);
+  return hipLaunchCooperativeKernel(fn, dim3(a.L * a.ntile * g.slices), dim3(g.waves * 64), params, 0, s);
 }
 
 }  // namespace plh

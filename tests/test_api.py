@@ -66,7 +66,7 @@ def test_unsupported_structures_fall_back_to_native(kwargs, name):
 
 
 def test_unsupported_size_falls_back_to_native():
-    conv = P.convert_regressor_module(make_regressor(5, 300, 2, 4))
+    conv = P.convert_regressor_module(make_regressor(5, 520, 1, 4))
     assert isinstance(conv, P.NativeModuleFallback)
     assert conv.backend_name == "native_pytorch_unsupported_geometry"
 

@@ -53,7 +53,8 @@ def test_abi_version_and_error_text(ext):
 
 @pytest.mark.parametrize("I,H,L,O,ok", [
     (5, 128, 4, 24, True), (5, 1, 1, 1, True), (32, 32, 2, 0, True), (64, 64, 8, 3, True), (128, 128, 1, 24, True),
-    (5, 129, 4, 24, False), (33, 32, 2, 4, False), (0, 128, 4, 24, False), (5, 128, 0, 24, False), (5, 128, 4, -1, False),
+    (5, 129, 4, 24, True), (5, 256, 4, 24, True), (5, 512, 4, 24, True), (300, 300, 2, 1, True),
+    (5, 513, 4, 24, False), (33, 32, 2, 4, False), (257, 256, 2, 4, False), (0, 128, 4, 24, False), (5, 128, 0, 24, False), (5, 128, 4, -1, False),
 ])
 def test_supported_geometries(ext, I, H, L, O, ok):
     assert ext.supports(I, H, L, O) is ok
@@ -62,7 +63,8 @@ def test_supported_geometries(ext, I, H, L, O, ok):
 def test_packed_bytes_closed_form(ext):
     # wpack: L * (HP/16 waves) * (2*HP/32 chunks) * 4 gates * 64 lanes * 16 B, then f32 bias, head, all 256-aligned
     a = lambda v: (v + 255) // 256 * 256  # noqa: E731
-    for I, H, L, O, HP in [(5, 128, 4, 24, 128), (5, 100, 2, 3, 128), (5, 40, 3, 7, 64), (5, 10, 1, 0, 32)]:
+    for I, H, L, O, HP in [(5, 128, 4, 24, 128), (5, 100, 2, 3, 128), (5, 40, 3, 7, 64), (5, 10, 1, 0, 32),
+                           (5, 256, 4, 24, 256), (5, 200, 2, 3, 256), (5, 512, 4, 24, 512), (7, 400, 1, 1, 512)]:
         wp = L * (HP // 16) * (HP // 16) * 4 * 64 * 16
         want = a(wp) + a(L * 4 * HP * 4) + a(O * HP * 4) + a(O * 4)
         assert ext.packed_bytes(I, H, L, O) == want
@@ -78,6 +80,18 @@ def test_workspace_bytes_grow_with_sequence(ext):
     assert b >= 3 * 512 * 1000 * 128 * 2
     with pytest.raises(ValueError):
         ext.workspace_bytes(5, 128, 4, 24, -1, 10)
+
+
+def test_sliced_workspace_holds_every_layer(ext):
+    # H > 128: the hidden units of a layer are split over several workgroups that exchange h_t through
+    # the hand-off buffer, so it covers all L layers: >= L * rows_per_launch * T * HP * 2 bytes.  Without a
+    # device the plan assumes 256 co-resident workgroups: 256 / (L * 4 slices) = 16 tiles of 16 rows at
+    # HP = 256, and 256 / (L * 16) = 4 tiles at HP = 512.
+    for H, rows in ((256, 256), (512, 64)):
+        b = ext.workspace_bytes(5, H, 4, 24, 512, 1000)
+        assert b >= 4 * rows * 1000 * H * 2
+        xp = rows * 1000 * 32 * 2  # x of the launch, padded to one 32-wide K chunk
+        assert b < 4 * rows * 1000 * H * 2 + xp + (1 << 16)
 
 
 def test_forward_validates_before_touching_the_device(ext):

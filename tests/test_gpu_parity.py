@@ -41,6 +41,10 @@ def _torch_ref(native, x, lengths=None):
     (5, 64, 3, 24, 33, 19),      # H bucket 64
     (17, 100, 2, 5, 16, 9),      # padded H and I > 8
     (5, 128, 4, 24, 48, 130),    # headline geometry, small batch
+    (5, 256, 2, 24, 20, 37),     # sliced: 4 workgroups per (layer, tile), ragged tile
+    (5, 200, 3, 5, 33, 19),      # sliced, padded H in the 256 bucket
+    (5, 512, 2, 24, 16, 21),     # sliced: 16 workgroups per (layer, tile)
+    (37, 300, 2, 3, 18, 11),     # sliced, padded H in the 512 bucket, I > 32
 ])
 def test_regressor_matches_oracle(gpu, I, H, L, O, B, T):
     _say(f"regressor I={I} H={H} L={L} O={O} B={B} T={T}")
@@ -221,3 +225,60 @@ def test_large_batches_use_16_row_tiles_and_split_launches(gpu, B, T):
     rows = np.r_[0:8, B // 2:B // 2 + 8, B - 8:B]
     ref = oracle.regressor_forward(x.numpy()[rows], oracle_layers(native.lstm), *linear_params(native.linear))
     assert_close(got.float().cpu().numpy()[rows], ref, what=f"B={B} vs oracle")
+
+
+@pytest.mark.parametrize("H,rows_checked", [(256, 512), (512, 48)])
+def test_large_hidden_c3_c4(gpu, H, rows_checked):
+    """C3 (H256) and C4 (H512): 4 layers, B512, T1000, served by the sliced kernel in several launches.
+
+    Output vs torch fp32 on `rows_checked` rows spread over every launch; h and c after 1, 100 and
+    1000 steps vs the oracle on rows of the first and the last launch.
+    """
+    I, L, O, B, T = 5, 4, 24, 512, 1000
+    _say(f"large hidden H={H} B={B} T={T}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    model = _gpu_model(native)
+    out, ph, pc = model.forward_probe(x.to("cuda", torch.float16), [1, 100, 1000])
+    gpu.check_status(torch.device("cuda"))
+    rows = np.arange(B) if rows_checked >= B else np.linspace(0, B - 1, rows_checked).astype(int)
+    want = _torch_ref(native, x[rows])
+    mx, mn = assert_close(out.float().cpu().numpy()[rows], want, what=f"H={H} out vs torch fp32")
+    _say(f"H={H} out vs torch fp32: max_abs={mx:.3e} mean_abs={mn:.3e}")
+    nprobe = 8 if H <= 256 else 4  # the scalar oracle takes ~1.5 s per row at H512
+    prow = np.r_[0:nprobe, B - nprobe:B]
+    ref = oracle.lstm_forward(x.numpy()[prow], oracle_layers(native.lstm), probe_steps=(1, 100, 1000))
+    for p, step in enumerate((1, 100, 1000)):
+        for name, got_all, want_all in (("h", ph, ref["probe_h"]), ("c", pc, ref["probe_c"])):
+            g = got_all[p][:, prow].cpu().numpy()
+            mx, mn = assert_close(g, want_all[p], what=f"H={H} {name} after {step} steps")
+            _say(f"H={H} {name}@{step}: max_abs={mx:.3e} mean_abs={mn:.3e}")
+
+
+def test_sliced_persistent_lstm_dropin_with_state(gpu):
+    """H256 PersistentLSTM with h0/c0, full output sequence and final state, plus ragged lengths."""
+    I, H, L, B, T = 24, 256, 2, 40, 33
+    _say("sliced PersistentLSTM drop-in")
+    torch.manual_seed(11)
+    lstm = torch.nn.LSTM(I, H, L, batch_first=True).eval()
+    x = make_x(B, T, I, seed=12)
+    g = torch.Generator().manual_seed(13)
+    h0 = 0.5 * torch.randn(L, B, H, generator=g)
+    c0 = 0.5 * torch.randn(L, B, H, generator=g)
+    with torch.inference_mode():
+        want_out, (want_h, want_c) = lstm(x, (h0, c0))
+    mod = PersistentLSTM.from_native_module(lstm).to("cuda").half()
+    out, (h, c) = mod(x.to("cuda", torch.float16), (h0.cuda().half(), c0.cuda().half()))
+    gpu.check_status(torch.device("cuda"))
+    assert_close(out.float().cpu().numpy(), want_out.numpy(), what="sliced out seq")
+    assert_close(h.float().cpu().numpy(), want_h.numpy(), what="sliced h_n")
+    assert_close(c.float().cpu().numpy(), want_c.numpy(), what="sliced c_n")
+    lengths = torch.tensor(sorted(torch.randint(0, T + 1, (B,), generator=g).tolist(), reverse=True))
+    lengths[0] = T
+    lengths[-1] = 0
+    native = make_regressor(I, H, L, 6)
+    model = _gpu_model(native)
+    got = model.forward_ragged(x.to("cuda", torch.float16), lengths).float().cpu().numpy()
+    want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
+                                    lengths=lengths.numpy())
+    assert_close(got, want, what="sliced ragged")

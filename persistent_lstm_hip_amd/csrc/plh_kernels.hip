@@ -473,9 +473,18 @@ lstm_wavefront_kernel(ForwardArgs a) {
 //   * per step each wave computes its partial gate sums with MFMA, the partials meet in LDS, and
 //     the group's waves split the gate math of its 16 units x 16 rows;
 //   * h_t of the slice goes to the hand-off buffer; the S slices count steps on one shared counter
-//     (agent-scope release add / acquire) and every slice reloads the full h_t from global memory
-//     for its next recurrent part.  The same counter drives the chunked hand-off to the next layer,
-//     so layers still run as a wavefront.
+//     and every slice reloads the full h_t from global memory for its next recurrent part.  The same
+//     counter drives the chunked hand-off to the next layer, so layers still run as a wavefront.
+//
+// The per-step exchange avoids agent-scope release/acquire fences, whose L2 write-back and
+// invalidate would otherwise dominate every step: each h element is written and re-read with
+// agent-scope relaxed atomic accesses (sc1: coherent across the XCDs' L2s without cache
+// maintenance), every thread waits for its stores to complete (s_waitcnt) before the workgroup
+// barrier that precedes the counter increment, and readers issue their loads only after observing
+// the counter.  These are the instruction sequences the AMDGPU memory model uses for agent-scope
+// release/acquire minus the L2 maintenance that only non-atomic accesses need.  The next layer
+// reads the buffer with ordinary loads after an agent-scope acquire (one per chunk), which
+// invalidates any stale copy in its L2.
 template <int HP>
 struct Sliced {
   static constexpr int kKsp = HP / 256;     // waves per K part of a unit group
@@ -486,6 +495,51 @@ struct Sliced {
   static constexpr int kWpg = 2 * kKsp;     // waves per unit group
   static constexpr int kUpw = 4 / kWpg;     // D rows (units) of a lane that each wave of the group evaluates
 };
+
+// wait_counter without the closing acquire: for data that is itself read with agent-scope atomic
+// loads.  Same bound and failure behaviour.
+__device__ int wait_counter_relaxed(const uint32_t* ctr, uint32_t need, uint32_t* status) {
+  uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (v < need) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      __builtin_amdgcn_s_sleep(1);
+      v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (v >= need) break;
+      if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return 0;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinLimitTicks) {
+        __hip_atomic_fetch_or(status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return 0;
+      }
+    }
+  }
+  return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
+}
+
+// Agent-scope relaxed (sc1) store of one or two consecutive halfs.
+template <int N>
+__device__ __forceinline__ void store_h_agent(_Float16* dst, const _Float16 (&h)[N]) {
+  static_assert(N == 1 || N == 2, "one or two halfs");
+  if constexpr (N == 2) {
+    union { _Float16 h[2]; uint32_t u; } v;
+    v.h[0] = h[0];
+    v.h[1] = h[1];
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(dst), v.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    union { _Float16 h; uint16_t u; } v;
+    v.h = h[0];
+    __hip_atomic_store(reinterpret_cast<uint16_t*>(dst), v.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Agent-scope relaxed (sc1) load of 8 halfs as two 64-bit loads.
+__device__ __forceinline__ f16x8 load_f16x8_agent(const f16x8* src) {
+  const uint64_t* p = reinterpret_cast<const uint64_t*>(src);
+  union { uint64_t u[2]; f16x8 v; } r;
+  r.u[0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  r.u[1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return r.v;
+}
 
 // Workgroup -> (layer, tile, slice).  With xcd_map the S slices of a (layer, tile) share an XCD.
 __device__ __forceinline__ void sliced_coords(int b, int L, int ntile, int S, int xcd_map, int& layer, int& tile,
@@ -617,6 +671,13 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   auto need_up = [&](int k) -> uint32_t { return (uint32_t)(S * min((k + 1) * CH, Tt)); };
 
   int wait_idx = 0;
+  // Step exchange among the slices: no acquire fence, the data is re-read with agent-scope loads.
+  auto wait_ctr_coherent = [&](const uint32_t* ctr, uint32_t need) -> bool {
+    const int slot = wait_idx++ & 1;
+    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter_relaxed(ctr, need, a.status);
+    __syncthreads();
+    return s_ok[slot] != 0;
+  };
   auto wait_ctr = [&](const uint32_t* ctr, uint32_t need) -> bool {
     const int slot = wait_idx++ & 1;
     if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(ctr, need, a.status);
@@ -721,8 +782,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       }
       {
         _Float16* dst = my_seq_h + (size_t)t * hstep * 8;
-#pragma unroll
-        for (int j = 0; j < UPW; ++j) dst[j] = hcur[j];
+        store_h_agent(dst, hcur);
       }
       if (layer == a.L - 1 && a.out_seq && row_ok) {
         _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
@@ -735,16 +795,18 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
         ++probe_i;
         probe_next = probe_i < a.n_probe ? a.probe_steps[probe_i] : -1;
       }
-      // Publish this slice's h_t, then wait for every slice's h_t and reload the full h.
+      // Publish this slice's h_t (stores complete before the barrier), then wait for every slice's
+      // h_t and reload the full h with agent-coherent loads.
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if (threadIdx.x == 0) __hip_atomic_fetch_add(my_ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-      if (!wait_ctr(my_ctr, (uint32_t)(S * (t + 1)))) {
+      if (threadIdx.x == 0) __hip_atomic_fetch_add(my_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!wait_ctr_coherent(my_ctr, (uint32_t)(S * (t + 1)))) {
         ok = false;
         break;
       }
       {
         const f16x8* hsrc = my_seq + (size_t)t * hstep;
-        for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) hbuf[idx] = hsrc[idx];
+        for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) hbuf[idx] = load_f16x8_agent(hsrc + idx);
       }
       lds_barrier();
     }

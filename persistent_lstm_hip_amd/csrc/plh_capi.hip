@@ -228,6 +228,7 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   a.blin = (const float*)(pk + p.blin);
   a.xp = (plh::f16x8_t*)(ws + w.xp);
   a.hseq = (plh::f16x8_t*)(ws + w.hseq);
+  a.xring = (uint64_t*)(ws + w.xring);
   a.counters = counters;
   a.status = status;
   a.h0 = (const _Float16*)h0;
@@ -259,6 +260,10 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     a.xcd_map = (g.slices > 1 ? (g.L * a.ntile) % 8 : a.ntile % 8) == 0 ? 1 : 0;
     err = plh::launch_zero_u32(counters, (size_t)g.L * a.ntile, s);
     if (err != hipSuccess) return fail_hip(err, "counter reset");
+    if (g.slices > 1) {  // tags restart at 1: clear the exchange ring of this launch's tiles
+      err = plh::launch_zero_u32((uint32_t*)a.xring, (size_t)g.L * a.ntile * 2 * g.HP * 8 * 2, s);
+      if (err != hipSuccess) return fail_hip(err, "exchange ring reset");
+    }
     err = plh::launch_pack_x(g, a, s);
     if (err != hipSuccess) return fail_hip(err, "x packing");
     if (timed && row0 == 0) {

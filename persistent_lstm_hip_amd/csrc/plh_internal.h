@@ -42,10 +42,12 @@ PackedLayout packed_layout(const Geometry& g);
 //   status   u32                                   PLH_STATUS_* bits
 //   counters u32 [L][ntile]                        steps published per (layer, tile)
 //   xp       f16x8 [ntile][T][kc_in0][4][R]        x in B-fragment order (layer 0 input)
-//   hseq     f16x8 [L'][ntile][T][kci][4][R]       h of layers 0..L'-1 in B-fragment order; L' = L-1,
-//                                                  or L when sliced (slices exchange h_t through it)
+//   hseq     f16x8 [L-1][ntile][T][kci][4][R]      h of layers 0..L-2 in B-fragment order
+//   xring    u64 [L][ntile][2][HP * 8]             sliced geometries only: per-step exchange of h
+//                                                  among the slices of a (layer, tile), tagged words
 struct WorkspaceLayout {
-  size_t status, counters, xp, hseq, total;
+  size_t status, counters, xp, hseq, xring, total;
+  size_t xring_words;  // u64 words of xring (0 unless sliced)
   int chunk_rows;  // batch rows per persistent launch (co-residency bound), multiple of tile_rows
   int tile_rows;   // batch rows per workgroup: 8 or 16
 };
@@ -60,6 +62,7 @@ struct ForwardArgs {
   const float* blin;
   f16x8_t* xp;                  // packed x, see WorkspaceLayout
   f16x8_t* hseq;                // inter-layer hand-off, see WorkspaceLayout
+  uint64_t* xring;              // sliced kernels: tagged h exchange ring, zeroed before each launch
   uint32_t* counters;           // [L][ntile] steps published per (layer, tile)
   uint32_t* status;             // PLH_STATUS_* bits
   const _Float16* h0;           // [L, B, H] or null

@@ -471,20 +471,25 @@ lstm_wavefront_kernel(ForwardArgs a) {
 //     (W_ih columns, 256 per wave) and KSP waves the recurrent part (W_hh columns), so every wave's
 //     resident weights are 8 K-chunks x 4 gates = 128 VGPRs;
 //   * per step each wave computes its partial gate sums with MFMA, the partials meet in LDS, and
-//     the group's waves split the gate math of its 16 units x 16 rows;
-//   * h_t of the slice goes to the hand-off buffer; the S slices count steps on one shared counter
-//     and every slice reloads the full h_t from global memory for its next recurrent part.  The same
-//     counter drives the chunked hand-off to the next layer, so layers still run as a wavefront.
+//     the group's waves split the gate math of its 16 units x 16 rows (two units per lane);
+//   * the slices exchange h_t every step through a small ring of tagged words (below); the next
+//     layer still receives h through the hand-off buffer and a per-(layer, tile) step counter
+//     published once per chunk, so layers run as a wavefront.
 //
-// The per-step exchange avoids agent-scope release/acquire fences, whose L2 write-back and
-// invalidate would otherwise dominate every step: each h element is written and re-read with
-// agent-scope relaxed atomic accesses (sc1: coherent across the XCDs' L2s without cache
-// maintenance), every thread waits for its stores to complete (s_waitcnt) before the workgroup
-// barrier that precedes the counter increment, and readers issue their loads only after observing
-// the counter.  These are the instruction sequences the AMDGPU memory model uses for agent-scope
-// release/acquire minus the L2 maintenance that only non-atomic accesses need.  The next layer
-// reads the buffer with ordinary loads after an agent-scope acquire (one per chunk), which
-// invalidates any stale copy in its L2.
+// Tagged exchange.  One step's h of a tile is HP x 16 halfs, stored as 64-bit words
+// {h[u], h[u+1], tag = t + 1} in B-fragment order ([HP/8][16 rows][4 pairs]).  A reader spins on
+// the words themselves until every tag it needs equals t + 1: no store-completion wait, barrier or
+// counter round trip sits between a slice's epilogue and its siblings' next step.  Every word is
+// written and read with agent-scope relaxed 64-bit atomics (sc1), which are single-copy atomic and
+// coherent across the XCDs' L2 caches without cache maintenance.  Two ring slots suffice: a slice
+// can overwrite slot t % 2 with h_{t+2} only after it has read h_{t+1} of every sibling, and a
+// sibling writes h_{t+1} only after it has read h_t from every slice.  The ring is zeroed before
+// each launch (tags start at 1).
+//
+// Hand-off to the next layer: h is also stored to the hand-off buffer with agent-scope relaxed
+// stores; at the end of each chunk every thread waits for its stores to complete (s_waitcnt)
+// before the barrier that precedes a relaxed counter increment.  The next layer reads the buffer
+// with ordinary loads after an agent-scope acquire, which invalidates any stale copy in its L2.
 template <int HP>
 struct Sliced {
   static constexpr int kKsp = HP / 256;     // waves per K part of a unit group
@@ -493,56 +498,25 @@ struct Sliced {
   static constexpr int kS = HP / kHs;       // workgroups per (layer, tile)
   static constexpr int kKch = HP / 32;      // K chunks of one part
   static constexpr int kWpg = 2 * kKsp;     // waves per unit group
-  static constexpr int kUpw = 4 / kWpg;     // D rows (units) of a lane that each wave of the group evaluates
+  static constexpr int kWords = HP * 8;     // tagged words of one step's h of a 16-row tile
 };
 
-// wait_counter without the closing acquire: for data that is itself read with agent-scope atomic
-// loads.  Same bound and failure behaviour.
-__device__ int wait_counter_relaxed(const uint32_t* ctr, uint32_t need, uint32_t* status) {
-  uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (v < need) {
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    for (;;) {
-      __builtin_amdgcn_s_sleep(1);
-      v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (v >= need) break;
-      if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return 0;
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinLimitTicks) {
-        __hip_atomic_fetch_or(status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return 0;
-      }
-    }
-  }
-  return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
+// Per-lane bound on the spin of a tagged-exchange wait: 2 s of s_memrealtime, checked every 16 polls.
+__device__ __forceinline__ uint64_t tag_word(_Float16 a, _Float16 b, uint32_t tag) {
+  union { _Float16 h[2]; uint32_t u; } v;
+  v.h[0] = a;
+  v.h[1] = b;
+  return (uint64_t)v.u | ((uint64_t)tag << 32);
 }
 
-// Agent-scope relaxed (sc1) store of one or two consecutive halfs.
-template <int N>
-__device__ __forceinline__ void store_h_agent(_Float16* dst, const _Float16 (&h)[N]) {
-  static_assert(N == 1 || N == 2, "one or two halfs");
-  if constexpr (N == 2) {
-    union { _Float16 h[2]; uint32_t u; } v;
-    v.h[0] = h[0];
-    v.h[1] = h[1];
-    __hip_atomic_store(reinterpret_cast<uint32_t*>(dst), v.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    union { _Float16 h; uint16_t u; } v;
-    v.h = h[0];
-    __hip_atomic_store(reinterpret_cast<uint16_t*>(dst), v.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
+__device__ __forceinline__ uint32_t word_tag(uint64_t w) { return (uint32_t)(w >> 32); }
 
-// Agent-scope relaxed (sc1) load of 8 halfs as two 64-bit loads.
-__device__ __forceinline__ f16x8 load_f16x8_agent(const f16x8* src) {
-  const uint64_t* p = reinterpret_cast<const uint64_t*>(src);
-  union { uint64_t u[2]; f16x8 v; } r;
-  r.u[0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  r.u[1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return r.v;
+__device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Workgroup -> (layer, tile, slice).  With xcd_map the S slices of a (layer, tile) share an XCD.
-__device__ __forceinline__ void sliced_coords(int b, int L, int ntile, int S, int xcd_map, int& layer, int& tile,
+__device__ __forceinline__ void sliced_coords(int b, int ntile, int S, int xcd_map, int& layer, int& tile,
                                               int& slice) {
   int grp;
   if (xcd_map) {
@@ -555,43 +529,55 @@ __device__ __forceinline__ void sliced_coords(int b, int L, int ntile, int S, in
   }
   layer = grp / ntile;
   tile = grp % ntile;
-  (void)L;
 }
 
 template <int HP, int CH>
 __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   using C = Sliced<HP>;
-  constexpr int KSP = C::kKsp, HS = C::kHs, S = C::kS, KCH = C::kKch, WPG = C::kWpg, UPW = C::kUpw;
-  constexpr int NT = 512, FV = 64;  // 16-row fragment blocks
-  constexpr int RN = (CH * KCH * FV + NT - 1) / NT;
-  constexpr int KCW = 8;            // K chunks per wave
+  constexpr int KSP = C::kKsp, HS = C::kHs, S = C::kS, KCH = C::kKch, WPG = C::kWpg;
+  constexpr int NT = 512, FV = 64;                  // 16-row fragment blocks
+  constexpr int RN = (CH * KCH * FV + NT - 1) / NT;  // f16x8 of a chunk's input each thread moves
+  constexpr int NF = KCH * FV / NT;                 // f16x8 of h each thread gathers per step
+  constexpr int KCW = 8;                            // K chunks per wave
+  static_assert(KCH * FV % NT == 0, "whole fragments per thread");
 
   __shared__ f16x8 ring[CH * KCH * FV];  // step inputs of the current chunk (all HP input units)
   __shared__ f16x8 hbuf[KCH * FV];       // h_{t-1} of all HP units
   __shared__ f32x4 part[8][4][64];       // partial gate sums of every wave
   __shared__ int s_ok[2];
+  __shared__ int s_fail;
   __shared__ int s_tlen;
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int n = lane & 15;
-  const int kg = lane >> 4;
   int layer, tile, slice;
-  sliced_coords(blockIdx.x, a.L, a.ntile, S, a.xcd_map, layer, tile, slice);
+  sliced_coords(blockIdx.x, a.ntile, S, a.xcd_map, layer, tile, slice);
   const int g = wave / WPG, ew = wave % WPG;
   const bool recurrent = ew >= KSP;  // this wave holds W_hh columns
   const int kq = ew % KSP;           // which 256-column quarter of its part
 
-  const int grow = a.row0 + tile * 16 + n;
+  // Epilogue mapping: each active lane evaluates units eu, eu + 1 of row en.  The partial sums of
+  // (unit 4 kgx + i, row en) sit in element i of lane 16 kgx + en of every wave of the group.
+  const int en = lane & 15;
+  const int kgx = WPG == 2 ? (lane >> 4) : ew;
+  const int pp = WPG == 2 ? ew : ((lane >> 4) & 1);
+  const bool active = WPG == 2 || lane < 32;
+  const int pl = kgx * 16 + en;
+  const int eu = slice * HS + g * 16 + kgx * 4 + 2 * pp;
+
+  const int grow = a.row0 + tile * 16 + en;
   const bool row_ok = grow < a.row_end;
   int len = 0;
   if (row_ok) {
     len = a.lengths ? a.lengths[grow] : a.T;
     len = len < 0 ? 0 : (len > a.T ? a.T : len);
   }
-  if (threadIdx.x == 0) s_tlen = 0;
+  if (threadIdx.x == 0) {
+    s_tlen = 0;
+    s_fail = 0;
+  }
   __syncthreads();
-  if (wave == 0 && kg == 0) atomicMax(&s_tlen, len);
+  if (wave == 0 && lane < 16) atomicMax(&s_tlen, len);
   __syncthreads();
   const int Tt = s_tlen;
 
@@ -604,19 +590,17 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
   }
-  const int u0 = slice * HS + g * 16 + kg * 4;  // units of this lane's 4 D rows
-  const int uo = u0 + ew * UPW;                 // the UPW of them this wave evaluates
-  float bq[4][UPW];
+  float bq[4][2];
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
-    for (int j = 0; j < UPW; ++j) bq[q][j] = a.bias[((size_t)layer * 4 + q) * HP + uo + j];
+    for (int j = 0; j < 2; ++j) bq[q][j] = a.bias[((size_t)layer * 4 + q) * HP + eu + j];
 
-  float c[UPW];
-  _Float16 hcur[UPW];
+  float c[2];
+  _Float16 hcur[2];
 #pragma unroll
-  for (int j = 0; j < UPW; ++j) {
-    const int u = uo + j;
+  for (int j = 0; j < 2; ++j) {
+    const int u = eu + j;
     const bool v = row_ok && u < a.H;
     const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
     c[j] = (v && a.c0) ? (float)a.c0[si] : 0.0f;
@@ -637,12 +621,15 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   }
 
   const bool has_up = layer > 0;
+  const bool has_down = layer + 1 < a.L;
   const int kin = has_up ? KCH : a.kc_in0;
   const size_t hstep = (size_t)KCH * FV;
   const f16x8* in_seq = has_up ? a.hseq + ((size_t)(layer - 1) * a.ntile + tile) * a.T * hstep
                                : a.xp + (size_t)tile * a.T * kin * FV;
-  f16x8* my_seq = a.hseq + ((size_t)layer * a.ntile + tile) * a.T * hstep;
-  _Float16* my_seq_h = reinterpret_cast<_Float16*>(my_seq) + ((uo >> 3) * 16 + n) * 8 + (uo & 7);
+  f16x8* my_seq = has_down ? a.hseq + ((size_t)layer * a.ntile + tile) * a.T * hstep : nullptr;
+  const int hoff = ((eu >> 3) * 16 + en) * 8 + (eu & 7);  // halfs: (row en, unit eu) in a step block
+  uint64_t* xr = a.xring + ((size_t)layer * a.ntile + tile) * 2 * C::kWords;
+  const int woff = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's word in a ring slot
   const uint32_t* up_ctr = has_up ? a.counters + (layer - 1) * a.ntile + tile : nullptr;
   uint32_t* my_ctr = a.counters + layer * a.ntile + tile;
   const int sync_tid = 64;
@@ -671,13 +658,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   auto need_up = [&](int k) -> uint32_t { return (uint32_t)(S * min((k + 1) * CH, Tt)); };
 
   int wait_idx = 0;
-  // Step exchange among the slices: no acquire fence, the data is re-read with agent-scope loads.
-  auto wait_ctr_coherent = [&](const uint32_t* ctr, uint32_t need) -> bool {
-    const int slot = wait_idx++ & 1;
-    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter_relaxed(ctr, need, a.status);
-    __syncthreads();
-    return s_ok[slot] != 0;
-  };
   auto wait_ctr = [&](const uint32_t* ctr, uint32_t need) -> bool {
     const int slot = wait_idx++ & 1;
     if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(ctr, need, a.status);
@@ -685,19 +665,71 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     return s_ok[slot] != 0;
   };
 
+  // Gather h_t of every slice from ring slot t % 2 into hbuf; false (uniformly) if any wait failed.
+  auto gather_h = [&](int t) -> bool {
+    const uint64_t* src = xr + (size_t)(t & 1) * C::kWords + threadIdx.x * 4;
+    const uint32_t want = (uint32_t)t + 1u;
+    uint64_t wv[NF][4];
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv[f][j] = load_agent_u64(src + f * NT * 4 + j);
+    uint64_t t0 = 0;
+    for (int spin = 0;; ++spin) {
+      bool ready = true;
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ready = ready && word_tag(wv[f][j]) == want;
+      if (ready) break;
+      if (spin == 0) {
+        t0 = __builtin_amdgcn_s_memrealtime();
+      } else if ((spin & 15) == 0) {
+        if (__hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+          s_fail = 1;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinLimitTicks) {
+          __hip_atomic_fetch_or(a.status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          s_fail = 1;
+          break;
+        }
+      }
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (word_tag(wv[f][j]) != want) wv[f][j] = load_agent_u64(src + f * NT * 4 + j);
+    }
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      union { uint32_t u[4]; f16x8 v; } h;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h.u[j] = (uint32_t)wv[f][j];
+      hbuf[threadIdx.x + f * NT] = h.v;
+    }
+    lds_barrier();
+    return s_fail == 0;
+  };
+
   int probe_i = 0;
   int probe_next = a.n_probe > 0 ? a.probe_steps[0] : -1;
   auto write_probe = [&](int pi) {
-    if (!row_ok) return;
+    if (!row_ok || !active) return;
 #pragma unroll
-    for (int j = 0; j < UPW; ++j) {
-      const int u = uo + j;
+    for (int j = 0; j < 2; ++j) {
+      const int u = eu + j;
       if (u < a.H) {
         const size_t o = (((size_t)pi * a.L + layer) * a.B + grow) * a.H + u;
         a.probe_h[o] = (float)hcur[j];
         a.probe_c[o] = c[j];
       }
     }
+  };
+  auto publish = [&](uint32_t steps) {  // hand-off stores of this chunk complete, then count them
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(my_ctr, steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
 
   for (int i = threadIdx.x; i < CH * KCH * FV; i += NT) ring[i] = f16x8{};
@@ -721,7 +753,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 
   for (int k = 0; ok && k < nchunk; ++k) {
     if (k > 0) {
-      __syncthreads();
+      publish((uint32_t)CH);
       store_chunk(k);
       const bool more = k + 1 < nchunk;
       const int slot = wait_idx++ & 1;
@@ -762,55 +794,53 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       for (int q = 0; q < 4; ++q) part[wave][q][lane] = acc[q];
       lds_barrier();
 
-      // Gate math of this wave's UPW units: sum the group's partials and the bias.
+      // Gate math of this lane's two units: the group's partial sums plus the bias.
       const bool live = t < len;
+      if (active) {
 #pragma unroll
-      for (int j = 0; j < UPW; ++j) {
-        const int i = ew * UPW + j;
-        float z[4];
+        for (int j = 0; j < 2; ++j) {
+          float z[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float sum = bq[q][j];
+          for (int q = 0; q < 4; ++q) {
+            float sum = bq[q][j];
 #pragma unroll
-          for (int e = 0; e < WPG; ++e) sum += part[g * WPG + e][q][lane][i];
-          z[q] = sum;
+            for (int e = 0; e < WPG; ++e) sum += part[g * WPG + e][q][pl][2 * pp + j];
+            z[q] = sum;
+          }
+          float cn = c[j], hn;
+          lstm_cell(z[0], z[1], z[2], z[3], cn, hn);
+          c[j] = live ? cn : c[j];
+          hcur[j] = live ? (_Float16)hn : hcur[j];
         }
-        float cn = c[j], hn;
-        lstm_cell(z[0], z[1], z[2], z[3], cn, hn);
-        c[j] = live ? cn : c[j];
-        hcur[j] = live ? (_Float16)hn : hcur[j];
-      }
-      {
-        _Float16* dst = my_seq_h + (size_t)t * hstep * 8;
-        store_h_agent(dst, hcur);
-      }
-      if (layer == a.L - 1 && a.out_seq && row_ok) {
-        _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
+        __hip_atomic_store(xr + (size_t)(t & 1) * C::kWords + woff, tag_word(hcur[0], hcur[1], (uint32_t)t + 1u),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (has_down) {
+          union { _Float16 h[2]; uint32_t u; } v;
+          v.h[0] = hcur[0];
+          v.h[1] = hcur[1];
+          __hip_atomic_store(reinterpret_cast<uint32_t*>(reinterpret_cast<_Float16*>(my_seq + (size_t)t * hstep) + hoff),
+                             v.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (!has_down && a.out_seq && row_ok) {
+          _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
 #pragma unroll
-        for (int j = 0; j < UPW; ++j)
-          if (uo + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
+          for (int j = 0; j < 2; ++j)
+            if (eu + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
+        }
       }
       if (t + 1 == probe_next) {
         write_probe(probe_i);
         ++probe_i;
         probe_next = probe_i < a.n_probe ? a.probe_steps[probe_i] : -1;
       }
-      // Publish this slice's h_t (stores complete before the barrier), then wait for every slice's
-      // h_t and reload the full h with agent-coherent loads.
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (threadIdx.x == 0) __hip_atomic_fetch_add(my_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (!wait_ctr_coherent(my_ctr, (uint32_t)(S * (t + 1)))) {
+      // h_t of every slice for the next step (and, after the last step, for the head).
+      if (!gather_h(t)) {
         ok = false;
         break;
       }
-      {
-        const f16x8* hsrc = my_seq + (size_t)t * hstep;
-        for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) hbuf[idx] = load_f16x8_agent(hsrc + idx);
-      }
-      lds_barrier();
     }
   }
+  if (ok && Tt > 0) publish((uint32_t)(Tt - (nchunk - 1) * CH));
 
   if (!ok) {
     if (layer == a.L - 1 && slice == 0 && a.out) {
@@ -822,22 +852,22 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     return;
   }
 
-  if (layer == a.L - 1 && a.out_seq && row_ok) {
+  if (!has_down && a.out_seq && row_ok && active) {
     for (int t = Tt; t < a.T; ++t) {
-      _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
+      _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
 #pragma unroll
-      for (int j = 0; j < UPW; ++j)
-        if (uo + j < a.H) dst[j] = (_Float16)0.0f;
+      for (int j = 0; j < 2; ++j)
+        if (eu + j < a.H) dst[j] = (_Float16)0.0f;
     }
   }
   while (probe_i < a.n_probe) {
     write_probe(probe_i);
     ++probe_i;
   }
-  if (row_ok) {
+  if (row_ok && active) {
 #pragma unroll
-    for (int j = 0; j < UPW; ++j) {
-      const int u = uo + j;
+    for (int j = 0; j < 2; ++j) {
+      const int u = eu + j;
       if (u < a.H) {
         const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
         if (a.h_n) a.h_n[si] = hcur[j];
@@ -846,7 +876,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     }
   }
   // Linear head (last layer, first slice) on the full final h held in hbuf.
-  if (layer == a.L - 1 && slice == 0 && a.out) {
+  if (!has_down && slice == 0 && a.out) {
     const _Float16* hf = reinterpret_cast<const _Float16*>(hbuf);
     for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
       const int rr = idx / a.O, o = idx % a.O;
@@ -1061,8 +1091,9 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   w.counters = 256;
   w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile);
   w.hseq = align256(w.xp + ntile * seq_len * g.kc_in0 * frag_bytes);
-  const size_t hseq_layers = g.slices > 1 ? g.L : g.L - 1;
-  w.total = align256(w.hseq + hseq_layers * ntile * seq_len * g.kci * frag_bytes);
+  w.xring = align256(w.hseq + (size_t)(g.L - 1) * ntile * seq_len * g.kci * frag_bytes);
+  w.xring_words = g.slices > 1 ? (size_t)g.L * ntile * 2 * g.HP * 8 : 0;
+  w.total = align256(w.xring + w.xring_words * sizeof(uint64_t));
   return w;
 }
 

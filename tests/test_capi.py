@@ -82,16 +82,20 @@ def test_workspace_bytes_grow_with_sequence(ext):
         ext.workspace_bytes(5, 128, 4, 24, -1, 10)
 
 
-def test_sliced_workspace_holds_every_layer(ext):
-    # H > 128: the hidden units of a layer are split over several workgroups that exchange h_t through
-    # the hand-off buffer, so it covers all L layers: >= L * rows_per_launch * T * HP * 2 bytes.  Without a
-    # device the plan assumes 256 co-resident workgroups: 256 / (L * 4 slices) = 16 tiles of 16 rows at
-    # HP = 256, and 256 / (L * 16) = 4 tiles at HP = 512.
-    for H, rows in ((256, 256), (512, 64)):
-        b = ext.workspace_bytes(5, H, 4, 24, 512, 1000)
-        assert b >= 4 * rows * 1000 * H * 2
-        xp = rows * 1000 * 32 * 2  # x of the launch, padded to one 32-wide K chunk
-        assert b < 4 * rows * 1000 * H * 2 + xp + (1 << 16)
+def test_sliced_workspace_layout(ext):
+    # H > 128: the hidden units of a layer are split over several workgroups ("slices").  The workspace
+    # holds the (L-1)-layer hand-off plus a two-step ring of tagged words per (layer, tile) through which
+    # the slices exchange h every step: L * tiles * 2 * (HP * 8) words of 8 bytes.  Without a device the
+    # plan assumes 256 co-resident workgroups: 256 / (L * 4 slices) = 16 tiles of 16 rows at HP = 256,
+    # and 256 / (L * 16) = 4 tiles at HP = 512.
+    L, T = 4, 1000
+    for H, tiles in ((256, 16), (512, 4)):
+        rows = tiles * 16
+        b = ext.workspace_bytes(5, H, L, 24, 512, T)
+        handoff = (L - 1) * rows * T * H * 2
+        ring = L * tiles * 2 * H * 8 * 8
+        xp = rows * T * 32 * 2  # x of the launch, padded to one 32-wide K chunk
+        assert handoff + ring + xp <= b < handoff + ring + xp + (1 << 12)
 
 
 def test_forward_validates_before_touching_the_device(ext):

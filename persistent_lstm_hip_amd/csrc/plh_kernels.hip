@@ -477,7 +477,9 @@ lstm_wavefront_kernel(ForwardArgs a) {
 //     published once per chunk, so layers run as a wavefront.
 //
 // Tagged exchange.  One step's h of a tile is HP x 16 halfs, stored as 64-bit words
-// {h[u], h[u+1], tag = t + 1} in B-fragment order ([HP/8][16 rows][4 pairs]).  A reader spins on
+// {h[u], h[u+1], tag = t + 1} in writer order ([slice][wave][lane], one word per active lane), so
+// each wave's stores and each reader's loads cover contiguous 512-byte runs; the reader scatters
+// the payloads into B-fragment order in LDS.  A reader spins on
 // the words themselves until every tag it needs equals t + 1: no store-completion wait, barrier or
 // counter round trip sits between a slice's epilogue and its siblings' next step.  Every word is
 // written and read with agent-scope relaxed 64-bit atomics (sc1), which are single-copy atomic and
@@ -537,7 +539,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   constexpr int KSP = C::kKsp, HS = C::kHs, S = C::kS, KCH = C::kKch, WPG = C::kWpg;
   constexpr int NT = 512, FV = 64;                  // 16-row fragment blocks
   constexpr int RN = (CH * KCH * FV + NT - 1) / NT;  // f16x8 of a chunk's input each thread moves
-  constexpr int NF = KCH * FV / NT;                 // f16x8 of h each thread gathers per step
   constexpr int KCW = 8;                            // K chunks per wave
   static_assert(KCH * FV % NT == 0, "whole fragments per thread");
 
@@ -629,7 +630,22 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   f16x8* my_seq = has_down ? a.hseq + ((size_t)layer * a.ntile + tile) * a.T * hstep : nullptr;
   const int hoff = ((eu >> 3) * 16 + en) * 8 + (eu & 7);  // halfs: (row en, unit eu) in a step block
   uint64_t* xr = a.xring + ((size_t)layer * a.ntile + tile) * 2 * C::kWords;
-  const int woff = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's word in a ring slot
+  constexpr int WL = WPG == 2 ? 64 : 32;  // tagged words each wave writes per step (its active lanes)
+  constexpr int NW = C::kWords / NT;       // tagged words each thread gathers per step
+  static_assert(S * 8 * WL == C::kWords && C::kWords % NT == 0, "writer-order ring covers one step");
+  const int woff = (slice * 8 + wave) * WL + (lane & (WL - 1));  // this lane's word in a ring slot
+  // LDS destination (u32 index into hbuf) of every word this thread gathers.
+  int gdst[NW];
+#pragma unroll
+  for (int r = 0; r < NW; ++r) {
+    const int wd = threadIdx.x + r * NT;
+    const int sl = wd / (8 * WL), wv_ = (wd / WL) % 8, ln = wd % WL;
+    const int g_ = wv_ / WPG, ew_ = wv_ % WPG;
+    const int kgx_ = WPG == 2 ? (ln >> 4) : ew_;
+    const int pp_ = WPG == 2 ? ew_ : ((ln >> 4) & 1);
+    const int eu_ = sl * HS + g_ * 16 + kgx_ * 4 + 2 * pp_;
+    gdst[r] = ((eu_ >> 3) * 16 + (ln & 15)) * 4 + ((eu_ & 7) >> 1);
+  }
   const uint32_t* up_ctr = has_up ? a.counters + (layer - 1) * a.ntile + tile : nullptr;
   uint32_t* my_ctr = a.counters + layer * a.ntile + tile;
   const int sync_tid = 64;
@@ -667,20 +683,16 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 
   // Gather h_t of every slice from ring slot t % 2 into hbuf; false (uniformly) if any wait failed.
   auto gather_h = [&](int t) -> bool {
-    const uint64_t* src = xr + (size_t)(t & 1) * C::kWords + threadIdx.x * 4;
+    const uint64_t* src = xr + (size_t)(t & 1) * C::kWords + threadIdx.x;
     const uint32_t want = (uint32_t)t + 1u;
-    uint64_t wv[NF][4];
+    uint64_t wv[NW];
 #pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) wv[f][j] = load_agent_u64(src + f * NT * 4 + j);
+    for (int r = 0; r < NW; ++r) wv[r] = load_agent_u64(src + r * NT);
     uint64_t t0 = 0;
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int f = 0; f < NF; ++f)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ready = ready && word_tag(wv[f][j]) == want;
+      for (int r = 0; r < NW; ++r) ready = ready && word_tag(wv[r]) == want;
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -696,18 +708,12 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
         }
       }
 #pragma unroll
-      for (int f = 0; f < NF; ++f)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (word_tag(wv[f][j]) != want) wv[f][j] = load_agent_u64(src + f * NT * 4 + j);
+      for (int r = 0; r < NW; ++r)
+        if (word_tag(wv[r]) != want) wv[r] = load_agent_u64(src + r * NT);
     }
+    uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf);
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      union { uint32_t u[4]; f16x8 v; } h;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) h.u[j] = (uint32_t)wv[f][j];
-      hbuf[threadIdx.x + f * NT] = h.v;
-    }
+    for (int r = 0; r < NW; ++r) hb32[gdst[r]] = (uint32_t)wv[r];
     lds_barrier();
     return s_fail == 0;
   };

@@ -803,18 +803,22 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       // Gate math of this lane's two units: the group's partial sums plus the bias.
       const bool live = t < len;
       if (active) {
+        float z[4][2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          z[q][0] = bq[q][0];
+          z[q][1] = bq[q][1];
+#pragma unroll
+          for (int e = 0; e < WPG; ++e) {
+            const float2 v = reinterpret_cast<const float2*>(&part[g * WPG + e][q][pl])[pp];
+            z[q][0] += v.x;
+            z[q][1] += v.y;
+          }
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          float z[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float sum = bq[q][j];
-#pragma unroll
-            for (int e = 0; e < WPG; ++e) sum += part[g * WPG + e][q][pl][2 * pp + j];
-            z[q] = sum;
-          }
           float cn = c[j], hn;
-          lstm_cell(z[0], z[1], z[2], z[3], cn, hn);
+          lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn, hn);
           c[j] = live ? cn : c[j];
           hcur[j] = live ? (_Float16)hn : hcur[j];
         }

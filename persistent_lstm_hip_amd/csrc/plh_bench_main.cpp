@@ -175,5 +175,6 @@ int main(int argc, char** argv) {
       "{\"geometry\": [%d, %d, %d, %d], \"batch\": %d, \"seq\": %d, \"iters\": %d, \"fwd_ms\": %.6f, "
       "\"kernel_ms\": %.6f, \"seq_steps_per_s\": %.6e, \"status\": %u, \"abs_checksum\": %.6f}\n",
       I, H, L, O, B, T, iters, fwd_ms, kern_ms, seq_steps / (fwd_ms * 1e-3), status, checksum);
+  std::fflush(stdout);  // profilers may end the process abnormally after main returns
   return status == 0 ? 0 : 2;
 }

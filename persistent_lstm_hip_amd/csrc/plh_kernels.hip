@@ -52,9 +52,11 @@ __device__ __forceinline__ float exp_neg(float z, float k) {
 // sigmoid(i), sigmoid(f), tanh(g), sigmoid(o), tanh(c') as 1 / (1 + e^-x):
 //   c' = sigmoid(f) c + sigmoid(i) tanh(g) = [c (1+ei)(1+eg) + (1-eg)(1+ef)] / [(1+ef)(1+ei)(1+eg)]
 //   h  = sigmoid(o) tanh(c')               = (1 - ec) / [(1+eo)(1+ec)]
-// where ex = e^{-x} for the logistic gates and e^{-2x} for the tanh arguments.
+// where ex = e^{-x} for the logistic gates and e^{-2x} for the tanh arguments.  eo alone needs no
+// cap: with ec capped, 1 - ec is finite, so eo = +inf gives h = finite * rcp(inf) = 0, the limit.
 __device__ __forceinline__ void lstm_cell(float zi, float zf, float zg, float zo, float& c, float& h) {
-  const float ei = exp_neg(zi, 1.0f), ef = exp_neg(zf, 1.0f), eg = exp_neg(zg, 2.0f), eo = exp_neg(zo, 1.0f);
+  const float ei = exp_neg(zi, 1.0f), ef = exp_neg(zf, 1.0f), eg = exp_neg(zg, 2.0f);
+  const float eo = __builtin_amdgcn_exp2f(zo * -kLog2e);
   const float a = 1.0f + ei, b = 1.0f + eg, d = 1.0f + ef;
   const float ab = a * b;
   const float cn = fmaf(c, ab, (1.0f - eg) * d) * __builtin_amdgcn_rcpf(d * ab);
@@ -127,7 +129,16 @@ __device__ __forceinline__ int frag_index(int r, int k) { return ((k >> 3) * ROW
 // The persistent layer-wavefront recurrence.  Template: padded hidden size HP, batch rows per
 // workgroup ROWS (16, or 8 with the MFMA's B columns 8..15 duplicating rows 0..7 so each lane
 // evaluates two (unit, row) pairs instead of four), steps per hand-off chunk CH.
-template <int HP, int ROWS, int CH>
+// a if !sel else b, as one v_cndmask: the empty asm hides that a and b are elements of one vector,
+// which would otherwise be turned into a dynamically indexed extract (three compares and selects).
+__device__ __forceinline__ float pick(bool sel, float a, float b) {
+  asm volatile("" : "+v"(b));
+  return sel ? b : a;
+}
+
+// RAGGED: rows may end before the tile's last step (lengths given); otherwise every row is live at
+// every step and the state-freezing selects are compiled out.
+template <int HP, int ROWS, int CH, bool RAGGED>
 __global__ void __launch_bounds__(HP / 16 * 64)
 lstm_wavefront_kernel(ForwardArgs a) {
   using C = Tile<HP, ROWS, CH>;
@@ -366,16 +377,20 @@ lstm_wavefront_kernel(ForwardArgs a) {
           const int kc = m / 4, q = m % 4;
           acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
         }
-        // this lane's pair j: D element ibase + j of every gate tile
-        const float zi = hi ? acc[0][2 + j % 2] : acc[0][j];
-        const float zf = hi ? acc[1][2 + j % 2] : acc[1][j];
-        const float zg = hi ? acc[2][2 + j % 2] : acc[2][j];
-        const float zo = hi ? acc[3][2 + j % 2] : acc[3][j];
+        // this lane's pair j: D element ibase + j of every gate tile (one v_cndmask each)
+        float z[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) z[q] = pick(hi, acc[q][j], acc[q][2 + j % 2]);
         float cn = c[j], hn;
-        lstm_cell(zi, zf, zg, zo, cn, hn);
-        // selects, not a branch: rows past their length keep their state
-        c[j] = live ? cn : c[j];
-        hcur[j] = live ? (_Float16)hn : hcur[j];
+        lstm_cell(z[0], z[1], z[2], z[3], cn, hn);
+        if constexpr (RAGGED) {
+          // selects, not a branch: rows past their length keep their state
+          c[j] = live ? cn : c[j];
+          hcur[j] = live ? (_Float16)hn : hcur[j];
+        } else {
+          c[j] = cn;
+          hcur[j] = (_Float16)hn;
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       *reinterpret_cast<hvec*>(hist_h(s)) = hcur;
@@ -1166,12 +1181,12 @@ hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, 
 #endif
 constexpr int kChunk = PLH_CHUNK_STEPS;
 
-template <int ROWS>
+template <int ROWS, bool RAGGED>
 static const void* recurrent_kernel_rows(int HP) {
   switch (HP) {
-    case 32: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<32, ROWS, kChunk>);
-    case 64: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<64, ROWS, kChunk>);
-    case 128: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<128, ROWS, kChunk>);
+    case 32: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<32, ROWS, kChunk, RAGGED>);
+    case 64: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<64, ROWS, kChunk, RAGGED>);
+    case 128: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<128, ROWS, kChunk, RAGGED>);
     default: return nullptr;
   }
 }
@@ -1180,7 +1195,7 @@ static const void* recurrent_kernel_rows(int HP) {
 constexpr int kChunk256 = 4;
 constexpr int kChunk512 = 2;
 
-static const void* recurrent_kernel(const Geometry& g, int tile_rows) {
+static const void* recurrent_kernel(const Geometry& g, int tile_rows, bool ragged) {
   if (g.slices > 1) {
     if (tile_rows != 16) return nullptr;
     switch (g.HP) {
@@ -1189,25 +1204,33 @@ static const void* recurrent_kernel(const Geometry& g, int tile_rows) {
       default: return nullptr;
     }
   }
-  return tile_rows == 8 ? recurrent_kernel_rows<8>(g.HP) : tile_rows == 16 ? recurrent_kernel_rows<16>(g.HP) : nullptr;
+  if (tile_rows == 8) return ragged ? recurrent_kernel_rows<8, true>(g.HP) : recurrent_kernel_rows<8, false>(g.HP);
+  if (tile_rows == 16) return ragged ? recurrent_kernel_rows<16, true>(g.HP) : recurrent_kernel_rows<16, false>(g.HP);
+  return nullptr;
 }
 
 int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err) {
-  const void* fn = recurrent_kernel(g, tile_rows);
-  if (!fn) {
-    *err = hipErrorInvalidValue;
-    return 0;
+  // The smaller occupancy of the two variants (with and without lengths), so either fits.
+  int cap = 0;
+  for (const bool ragged : {false, true}) {
+    const void* fn = recurrent_kernel(g, tile_rows, ragged);
+    if (!fn) {
+      *err = hipErrorInvalidValue;
+      return 0;
+    }
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, g.waves * 64, 0);
+    *err = e;
+    if (e != hipSuccess) return 0;
+    cap = (cap == 0 || per_cu * cus < cap) ? per_cu * cus : cap;
   }
-  int dev = 0, cus = 0, per_cu = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, g.waves * 64, 0);
-  *err = e;
-  return e == hipSuccess ? per_cu * cus : 0;
+  return cap;
 }
 
 hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s) {
-  const void* fn = recurrent_kernel(g, a.tile_rows);
+  const void* fn = recurrent_kernel(g, a.tile_rows, a.lengths != nullptr);
   if (!fn) return hipErrorInvalidValue;
   ForwardArgs args = a;
   void* params[] = {&args};

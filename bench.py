@@ -44,6 +44,11 @@ def algorithmic_flops(I, H, L, O, B, T) -> float:
     return 2.0 * B * T * 4 * H * ((I + H) + (L - 1) * 2 * H) + 2.0 * B * H * O
 
 
+def input_projection_flops(I, H, L, B, T) -> float:
+    """FLOPs of the input projections x_t W_ih^T of all layers: 2*B*T*4H*[I + (L-1)*H]."""
+    return 2.0 * B * T * 4 * H * (I + (L - 1) * H)
+
+
 def _profile_value(path, key):
     """A `key: value` line of a committed rocprofv3 summary under profiles/, or None."""
     try:
@@ -199,7 +204,7 @@ def main() -> int:
         "latency_s": median_ms * 1e-3,
         "latency_100_fwd_wall_s": wall * 100.0 / args.steps,
         "kernel": {
-            "name": "lstm_wavefront_kernel<128,8,8>",
+            "name": "lstm_wavefront_kernel<128,8,8,false>",
             "avg_ms": kernel_ms,
             "per_step_us": kernel_ms * 1e3 / (T + L - 1),
             "timed_launches": n_timed,
@@ -212,6 +217,15 @@ def main() -> int:
             "frac": achieved / PEAK_FP16_TFLOPS,
             "traffic": read_traffic(),
             "flops_per_launch": flops,
+        },
+        "input_projection": {
+            "fused": True,
+            "note": "the time-parallel input GEMM is fused into the persistent kernel: each step's x_t W_ih^T "
+                    "runs on MFMA, software-pipelined under the previous step's gate math; achieved = its "
+                    "algorithmic FLOPs / the kernel's duration",
+            "flops_per_launch": input_projection_flops(I, H, L, B, T),
+            "achieved_tflops": input_projection_flops(I, H, L, B, T) / (kernel_ms * 1e-3) / 1e12,
+            "frac_of_peak": input_projection_flops(I, H, L, B, T) / (kernel_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
         },
         "mfma_util": {
             "algorithmic_percent": 100.0 * achieved / PEAK_FP16_TFLOPS,

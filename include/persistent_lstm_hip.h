@@ -115,6 +115,15 @@ int plh_status(const void* workspace, uint32_t* status, void* stream);
 int plh_kernel_timing(int max_forwards);
 int plh_kernel_timing_read(double* total_ms, int* forwards);
 
+/*
+ * Bound on every wait between workgroups of the calling thread's later plh_forward calls, in
+ * microseconds (default 2000000; limit_us <= 0 restores the default).  A wait that exceeds it sets
+ * PLH_STATUS_TIMEOUT, fails every other wait of the launch and poisons the outputs with NaN, so
+ * the kernel always ends.  Failure detection for hung co-resident workgroups; no counterpart in the
+ * reference (its kernels spin without bound).
+ */
+int plh_set_wait_limit_us(int64_t limit_us);
+
 /* out[r, c] = in[0, c] for r < rows (fp16).  Replaces repeat_first_row
  * (bindings.cpp:164, persistent_lstm_hip.cu:1684-1695, :1784-1809). */
 int plh_repeat_first_row(const void* in, void* out, int rows, int cols, void* stream);

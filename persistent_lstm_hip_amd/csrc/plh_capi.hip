@@ -118,6 +118,10 @@ struct KernelTiming {
 };
 thread_local KernelTiming g_timing;
 
+// Bound on inter-workgroup waits of this thread's forwards (plh_set_wait_limit_us).
+constexpr int64_t kDefaultWaitUs = 2000000;
+thread_local int64_t g_wait_us = kDefaultWaitUs;
+
 }  // namespace
 
 extern "C" {
@@ -248,6 +252,7 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   a.L = g.L;
   a.O = g.O;
   a.kc_in0 = g.kc_in0;
+  a.wait_ticks = (uint64_t)g_wait_us * 100u;  // s_memrealtime: 100 MHz
 
   const bool timed = g_timing.used * 2 < (int)g_timing.ev.size();
   for (int row0 = 0; row0 < batch; row0 += chunk_rows) {
@@ -316,6 +321,11 @@ int plh_status(const void* workspace, uint32_t* status, void* stream) {
   hipError_t e = hipMemcpyAsync(status, workspace, sizeof(uint32_t), hipMemcpyDeviceToHost, (hipStream_t)stream);
   if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "status read");
+  return PLH_OK;
+}
+
+int plh_set_wait_limit_us(int64_t limit_us) {
+  g_wait_us = limit_us > 0 ? limit_us : kDefaultWaitUs;
   return PLH_OK;
 }
 

@@ -81,6 +81,7 @@ struct ForwardArgs {
   int tile_rows;                // batch rows per workgroup: 8 or 16
   int kc_in0;
   int xcd_map;                  // 1: keep a tile's layer chain on one XCD
+  uint64_t wait_ticks;          // bound on one inter-workgroup wait, in s_memrealtime ticks (100 MHz)
 };
 
 hipError_t launch_pack_layer(const Geometry& g, int layer, const _Float16* w_ih, const _Float16* w_hh,

@@ -37,8 +37,6 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
-// Wall-clock bound on one hand-off wait (s_memrealtime runs at 100 MHz): 2 s.
-constexpr uint64_t kSpinLimitTicks = 200000000ull;
 
 // e^{-k z} as 2^(min(-k z log2 e, 40)) on v_exp_f32.  The cap keeps a product of three (1 + e)
 // factors below 2^121 (no overflow) and moves no gate by more than 1e-12 (logistic(-27.7) ~ 1e-12).
@@ -72,9 +70,9 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Spin (one lane) until *ctr >= need, bounded in wall-clock time, then acquire at agent scope.
-// Returns 0 if the wait timed out or any workgroup of the grid has failed.
-__device__ int wait_counter(const uint32_t* ctr, uint32_t need, uint32_t* status) {
+// Spin (one lane) until *ctr >= need, bounded by `limit` ticks of s_memrealtime (100 MHz), then
+// acquire at agent scope.  Returns 0 if the wait timed out or any workgroup of the grid has failed.
+__device__ int wait_counter(const uint32_t* ctr, uint32_t need, uint32_t* status, uint64_t limit) {
   uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (v < need) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -83,7 +81,7 @@ __device__ int wait_counter(const uint32_t* ctr, uint32_t need, uint32_t* status
       v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (v >= need) break;
       if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return 0;
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinLimitTicks) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
         __hip_atomic_fetch_or(status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return 0;
       }
@@ -254,7 +252,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
   int wait_idx = 0;
   auto wait_up = [&](uint32_t need) -> bool {  // blocking wait for the upstream layer
     const int slot = wait_idx++ & 1;
-    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(up_ctr, need, a.status);
+    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(up_ctr, need, a.status, a.wait_ticks);
     __syncthreads();
     return s_ok[slot] != 0;
   };
@@ -310,7 +308,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
           okv = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
         } else {
-          okv = wait_counter(up_ctr, need, a.status);
+          okv = wait_counter(up_ctr, need, a.status, a.wait_ticks);
         }
         poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_ok[slot] = okv;
@@ -518,7 +516,6 @@ struct Sliced {
   static constexpr int kWords = HP * 8;     // tagged words of one step's h of a 16-row tile
 };
 
-// Per-lane bound on the spin of a tagged-exchange wait: 2 s of s_memrealtime, checked every 16 polls.
 __device__ __forceinline__ uint64_t tag_word(_Float16 a, _Float16 b, uint32_t tag) {
   union { _Float16 h[2]; uint32_t u; } v;
   v.h[0] = a;
@@ -691,7 +688,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   int wait_idx = 0;
   auto wait_ctr = [&](const uint32_t* ctr, uint32_t need) -> bool {
     const int slot = wait_idx++ & 1;
-    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(ctr, need, a.status);
+    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(ctr, need, a.status, a.wait_ticks);
     __syncthreads();
     return s_ok[slot] != 0;
   };
@@ -716,7 +713,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
           s_fail = 1;
           break;
         }
-        if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinLimitTicks) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
           __hip_atomic_fetch_or(a.status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           s_fail = 1;
           break;
@@ -785,7 +782,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
           okv = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
         } else {
-          okv = wait_counter(up_ctr, need, a.status);
+          okv = wait_counter(up_ctr, need, a.status, a.wait_ticks);
         }
         poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_ok[slot] = okv;

@@ -62,6 +62,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plh_kernel_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i32)]
     lib.plh_repeat_first_row.restype = _i32
     lib.plh_repeat_first_row.argtypes = [_vp, _vp, _i32, _i32, _vp]
+    lib.plh_set_wait_limit_us.restype = _i32
+    lib.plh_set_wait_limit_us.argtypes = [_i64]
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -70,6 +72,13 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def _device_key(device: torch.device) -> tuple:
+    """(type, index, current stream) with the index resolved, so "cuda" and "cuda:0" name one device."""
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return (device.type, index, _stream(torch.device(device.type, index)))
 
 
 class NativeLibrary:
@@ -170,7 +179,7 @@ class NativeLibrary:
     def workspace(self, device: torch.device, nbytes: int) -> torch.Tensor:
         """A cached workspace of at least nbytes per (device, stream): calls on one stream are
         ordered by it; calls on different streams get different workspaces."""
-        key = (device.type, device.index, _stream(device))
+        key = _device_key(device)
         ws = self._workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
             ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
@@ -268,7 +277,7 @@ class NativeLibrary:
 
     def status(self, device: torch.device) -> int:
         """Synchronise the current stream and return the device status word of the last forward."""
-        ws = self._workspaces.get((device.type, device.index, _stream(device)))
+        ws = self._workspaces.get(_device_key(device))
         if ws is None:
             return 0
         st = ctypes.c_uint32(0)
@@ -282,6 +291,11 @@ class NativeLibrary:
             raise RuntimeError("persistent LSTM kernel: a layer hand-off wait timed out (outputs are invalid)")
         if st:
             raise RuntimeError(f"persistent LSTM kernel reported status {st:#x}")
+
+    def set_wait_limit(self, seconds: Optional[float]) -> None:
+        """Bound on inter-workgroup waits of this thread's later forwards (None: the 2 s default)."""
+        us = 0 if seconds is None else max(1, int(round(seconds * 1e6)))
+        self._check(self.lib.plh_set_wait_limit_us(us), "plh_set_wait_limit_us")
 
     # ---- timing of the persistent kernel alone ----------------------------------------------
     def kernel_timing(self, max_forwards: int) -> None:

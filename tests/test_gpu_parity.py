@@ -282,3 +282,29 @@ def test_sliced_persistent_lstm_dropin_with_state(gpu):
     want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
                                     lengths=lengths.numpy())
     assert_close(got, want, what="sliced ragged")
+
+
+@pytest.mark.parametrize("H", [128, 256])
+def test_wait_timeout_is_reported_and_recovers(gpu, H):
+    """A forced 1 us wait bound: the next layer's first hand-off wait cannot be met, so the kernel sets
+    the timeout status, poisons the outputs and ends; the front end raises; the default bound then
+    gives correct results again (the status word is cleared by every forward)."""
+    I, L, O, B, T = 5, 2, 3, 16, 64
+    _say(f"forced wait timeout H={H}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    model = _gpu_model(native)
+    xg = x.to("cuda", torch.float16)
+    gpu.set_wait_limit(1e-6)
+    try:
+        out = model(xg)
+        torch.cuda.synchronize()
+        with pytest.raises(RuntimeError, match="timed out"):
+            gpu.check_status(torch.device("cuda"))
+        assert torch.isnan(out.float()).any(), "a timed-out forward must poison its outputs"
+    finally:
+        gpu.set_wait_limit(None)
+    got = model(xg)
+    gpu.check_status(torch.device("cuda"))
+    want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear))
+    assert_close(got.float().cpu().numpy(), want, what="after timeout")

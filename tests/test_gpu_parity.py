@@ -308,3 +308,53 @@ def test_wait_timeout_is_reported_and_recovers(gpu, H):
     gpu.check_status(torch.device("cuda"))
     want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear))
     assert_close(got.float().cpu().numpy(), want, what="after timeout")
+
+
+@pytest.mark.parametrize("I,H,L,O,B,T,zero_tail", [
+    (5, 128, 1, 4, 1, 1, False),      # one row, one step
+    (128, 128, 2, 4, 9, 17, False),   # input as wide as the padded hidden size
+    (5, 256, 1, 4, 3, 5, False),      # sliced kernel with a single layer (no hand-off)
+    (5, 512, 2, 4, 100, 9, False),    # sliced, 64-row launches: the second launch is partial
+    (5, 256, 2, 4, 20, 12, True),     # sliced: rows 16..19 have length 0, so one tile runs no step
+    (5, 128, 3, 4, 20, 12, True),     # wavefront: the same with 8-row tiles
+])
+def test_edge_geometries(gpu, I, H, L, O, B, T, zero_tail):
+    _say(f"edge I={I} H={H} L={L} O={O} B={B} T={T} zero_tail={zero_tail}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I, seed=21)
+    model = _gpu_model(native)
+    xg = x.to("cuda", torch.float16)
+    if zero_tail:
+        lengths = torch.randint(1, T + 1, (B,), generator=torch.Generator().manual_seed(22))
+        lengths[16:] = 0
+        got = model.forward_ragged(xg, lengths)
+        want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
+                                        lengths=lengths.numpy())
+    else:
+        got = model(xg)
+        want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear))
+    gpu.check_status(torch.device("cuda"))
+    assert_close(got.float().cpu().numpy(), want, what="edge geometry")
+    if zero_tail:  # zero steps: the head sees h = 0
+        np.testing.assert_allclose(got[16:].float().cpu().numpy(),
+                                   np.broadcast_to(native.linear.bias.detach().numpy(), (B - 16, O)), atol=2e-3)
+
+
+def test_sliced_side_stream_and_determinism(gpu):
+    """H512 on a non-default stream (its own workspace) equals the default-stream result bit for bit."""
+    I, H, L, O, B, T = 5, 512, 2, 6, 40, 30
+    _say("sliced side stream")
+    native = make_regressor(I, H, L, O)
+    model = _gpu_model(native)
+    xg = make_x(B, T, I).to("cuda", torch.float16)
+    a = model(xg)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        b = model(xg)
+        gpu.check_status(torch.device("cuda"))
+    torch.cuda.current_stream().wait_stream(s)
+    c = model(xg)
+    gpu.check_status(torch.device("cuda"))
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(a, c)

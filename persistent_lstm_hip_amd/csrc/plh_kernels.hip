@@ -514,6 +514,13 @@ struct Sliced {
   static constexpr int kKch = HP / 32;      // K chunks of one part
   static constexpr int kWpg = 2 * kKsp;     // waves per unit group
   static constexpr int kWords = HP * 8;     // tagged words of one step's h of a 16-row tile
+  // Wave roles: waves 0..3 hold W_ih parts, waves 4..7 W_hh parts, so each SIMD (wave w % 4) runs one
+  // of each and the input waves' MFMAs for step t+1 overlap the recurrent critical path of step t.
+  // Wave w serves unit group (w % 4) / KSP as member e = (w / 4) * KSP + w % KSP of the group
+  // (e < KSP: input part, quarter e; else recurrent part, quarter e - KSP).
+  static __host__ __device__ constexpr int group_of(int w) { return (w & 3) / kKsp; }
+  static __host__ __device__ constexpr int member_of(int w) { return (w >> 2) * kKsp + (w & (kKsp - 1)); }
+  static __host__ __device__ constexpr int wave_of(int g, int e) { return (e / kKsp) * 4 + g * kKsp + e % kKsp; }
 };
 
 __device__ __forceinline__ uint64_t tag_word(_Float16 a, _Float16 b, uint32_t tag) {
@@ -556,7 +563,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 
   __shared__ f16x8 ring[CH * KCH * FV];  // step inputs of the current chunk (all HP input units)
   __shared__ f16x8 hbuf[KCH * FV];       // h_{t-1} of all HP units
-  __shared__ f32x4 part[8][4][64];       // partial gate sums of every wave
+  __shared__ f32x4 part[2][8][4][64];    // partial gate sums of every wave, double-buffered by step
   __shared__ int s_ok[2];
   __shared__ int s_fail;
   __shared__ int s_tlen;
@@ -565,7 +572,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   const int lane = threadIdx.x & 63;
   int layer, tile, slice;
   sliced_coords(blockIdx.x, a.ntile, S, a.xcd_map, layer, tile, slice);
-  const int g = wave / WPG, ew = wave % WPG;
+  const int g = C::group_of(wave), ew = C::member_of(wave);
   const bool recurrent = ew >= KSP;  // this wave holds W_hh columns
   const int kq = ew % KSP;           // which 256-column quarter of its part
 
@@ -652,7 +659,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   for (int r = 0; r < NW; ++r) {
     const int wd = threadIdx.x + r * NT;
     const int sl = wd / (8 * WL), wv_ = (wd / WL) % 8, ln = wd % WL;
-    const int g_ = wv_ / WPG, ew_ = wv_ % WPG;
+    const int g_ = C::group_of(wv_), ew_ = C::member_of(wv_);
     const int kgx_ = WPG == 2 ? (ln >> 4) : ew_;
     const int pp_ = WPG == 2 ? ew_ : ((ln >> 4) & 1);
     const int eu_ = sl * HS + g_ * 16 + kgx_ * 4 + 2 * pp_;
@@ -693,13 +700,32 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     return s_ok[slot] != 0;
   };
 
+  // This wave's partial gate sums for step t: its K part of [ring slot s | h_{t-1}] times its weights.
+  auto partials = [&](int t, int s) {
+    const f16x8* src = (recurrent ? hbuf : ring + s * (KCH * FV)) + kq * KCW * FV + lane;
+    f32x4 acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < KCW; ++kc) {
+      const f16x8 bv = src[kc * FV];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], bv, acc[q], 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) part[t & 1][wave][q][lane] = acc[q];
+  };
+
   // Gather h_t of every slice from ring slot t % 2 into hbuf; false (uniformly) if any wait failed.
-  auto gather_h = [&](int t) -> bool {
+  // While the loads are in flight the input waves compute step t+1's partials (ring slot s_next,
+  // if it is in the current chunk).
+  auto gather_h = [&](int t, int s_next) -> bool {
     const uint64_t* src = xr + (size_t)(t & 1) * C::kWords + threadIdx.x;
     const uint32_t want = (uint32_t)t + 1u;
     uint64_t wv[NW];
 #pragma unroll
     for (int r = 0; r < NW; ++r) wv[r] = load_agent_u64(src + r * NT);
+    if (!recurrent && s_next >= 0) partials(t + 1, s_next);
     uint64_t t0 = 0;
     for (int spin = 0;; ++spin) {
       bool ready = true;
@@ -797,19 +823,9 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     const int ns = min(CH, Tt - k * CH);
     for (int s = 0; s < ns && ok; ++s) {
       const int t = k * CH + s;
-      // Partial gate sums of this wave's K part.
-      const f16x8* src = (recurrent ? hbuf : ring + s * (KCH * FV)) + kq * KCW * FV + lane;
-      f32x4 acc[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < KCW; ++kc) {
-        const f16x8 bv = src[kc * FV];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], bv, acc[q], 0, 0, 0);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) part[wave][q][lane] = acc[q];
+      // Partial gate sums: the recurrent waves now; the input waves computed theirs during the
+      // previous step's exchange, except on a chunk's first step (its input was not in LDS yet).
+      if (recurrent || s == 0) partials(t, s);
       lds_barrier();
 
       // Gate math of this lane's two units: the group's partial sums plus the bias.
@@ -822,7 +838,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
           z[q][1] = bq[q][1];
 #pragma unroll
           for (int e = 0; e < WPG; ++e) {
-            const float2 v = reinterpret_cast<const float2*>(&part[g * WPG + e][q][pl])[pp];
+            const float2 v = reinterpret_cast<const float2*>(&part[t & 1][C::wave_of(g, e)][q][pl])[pp];
             z[q][0] += v.x;
             z[q][1] += v.y;
           }
@@ -856,7 +872,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
         probe_next = probe_i < a.n_probe ? a.probe_steps[probe_i] : -1;
       }
       // h_t of every slice for the next step (and, after the last step, for the head).
-      if (!gather_h(t)) {
+      if (!gather_h(t, s + 1 < ns ? s + 1 : -1)) {
         ok = false;
         break;
       }
@@ -953,7 +969,8 @@ __global__ void pack_layer_kernel(const _Float16* __restrict__ w_ih, const _Floa
 }
 
 // Sliced weights: [L][S][8 waves][8 chunks][4 gates][64 lanes][8].  Wave w of slice s holds unit
-// group g = w / WPG, part ew / KSP (0: W_ih, 1: W_hh), quarter ew % KSP of that part's columns.
+// group Sliced::group_of(w); member e = Sliced::member_of(w) selects the part e / KSP (0: W_ih,
+// 1: W_hh) and the quarter e % KSP of that part's columns.
 template <int HP>
 __global__ void pack_sliced_kernel(const _Float16* __restrict__ w_ih, const _Float16* __restrict__ w_hh, int K,
                                    int H, _Float16* __restrict__ dst) {
@@ -967,7 +984,7 @@ __global__ void pack_sliced_kernel(const _Float16* __restrict__ w_ih, const _Flo
   const int kc = (int)((e >> 11) & 7);
   const int wv = (int)((e >> 14) & 7);
   const int sl = (int)(e >> 17);
-  const int g = wv / C::kWpg, ew = wv % C::kWpg;
+  const int g = C::group_of(wv), ew = C::member_of(wv);
   const bool rec = ew >= C::kKsp;
   const int kq = ew % C::kKsp;
   const int u = sl * C::kHs + g * 16 + (lane & 15);

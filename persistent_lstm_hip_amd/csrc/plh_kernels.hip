@@ -1,25 +1,32 @@
 // plh_kernels.hip -- CDNA4 (gfx950) kernels of the stacked LSTM + Linear inference forward.
 //
-// The hot kernel is a persistent, weight-stationary, layer-wavefront recurrence:
+// Two persistent, weight-stationary, layer-wavefront recurrences (cooperative launches: every
+// workgroup of a launch is co-resident and loops over the time steps itself):
 //
-//   * one workgroup per (layer l, batch tile of 16 rows); all L * ntile workgroups are co-resident
-//     (cooperative launch) and loop over the time steps themselves;
+// lstm_wavefront_kernel (H <= 128): one workgroup per (layer, batch tile of 8 or 16 rows).
 //   * each wave owns 16 hidden units and keeps the i, f, g, o rows of [W_ih | W_hh] for them in
-//     VGPRs for the whole sequence as fp16 MFMA A fragments (128 KB + 128 KB per layer at H = 128);
-//   * per step a wave computes gates^T[64 gate cols, 16 rows] = W[64, K] * [in_t | h_{t-1}]^T[K, 16]
-//     with v_mfma_f32_16x16x32_f16 (fp32 accumulate, bias as the initial accumulator); the gate
-//     nonlinearities and the c/h update run on the accumulator registers; c never leaves VGPRs;
-//   * activations live in "fragment order": a [16 rows x 32k] block is stored as [k/8][row][8],
-//     i.e. exactly the B operand of one MFMA (lane l reads 16 B at l * 16).  h_t goes to LDS in that
-//     order (double-buffered) for the tile's next step and, for l < L-1, to a global hand-off buffer
-//     in the same order, so LDS reads/writes are conflict-free and global traffic is contiguous;
-//   * the step input (x for layer 0, h^{l-1} otherwise) reaches LDS one chunk of `CH` steps at a
-//     time: the chunk is loaded to VGPRs during the previous chunk and written to an LDS ring at the
-//     chunk boundary, so no step waits on global memory;
+//     VGPRs for the whole sequence as fp16 MFMA A fragments (256 KB per layer at H = 128);
+//   * per step a wave computes gates^T[64 gate cols, 16 cols] = W[64, K] * [in_t | h_{t-1}]^T with
+//     v_mfma_f32_16x16x32_f16 (fp32 accumulate, bias as the initial accumulator); with 8-row tiles
+//     the B columns 8..15 repeat rows 0..7 and each lane evaluates two of its four (unit, row)
+//     pairs; the next step's input part is issued between this step's gate computations;
+//   * the gate nonlinearities and the c/h update run on the accumulator registers; c never leaves
+//     VGPRs; h goes to an LDS history ring that also feeds the next step's recurrent MFMAs;
+//   * activations live in "fragment order": a [R rows x 32 k] block is stored as [k/8][row][8],
+//     i.e. exactly the B operand of one MFMA (lane l reads 16 B at l * 16), in LDS and in the
+//     global hand-off buffer, so LDS traffic is conflict-free and global traffic contiguous;
+//   * the step input (x for layer 0, h of layer l-1 otherwise) reaches LDS one chunk of CH steps at
+//     a time, loaded to VGPRs during the previous chunk, so no step waits on global memory;
 //   * the hand-off between layers is a per-(layer, tile) step counter published with an agent-scope
-//     release at chunk boundaries and observed with a deferred poll + agent-scope acquire one chunk
-//     ahead: layer l+1 works on chunk k while layer l works on later chunks (layer wavefront);
+//     release once per chunk and observed with a deferred poll + agent-scope acquire one chunk
+//     ahead: layer l+1 works on chunk k while layer l works on later chunks;
 //   * the Linear head runs in the last layer's epilogue on the final h held in LDS.
+//
+// lstm_sliced_kernel (H 129..512): a layer's weights exceed one CU's registers, so S workgroups
+// ("slices") share a (layer, 16-row tile) and exchange h every step (see the section below).
+//
+// Every wait between workgroups is bounded in wall-clock time; a failed wait sets a status bit,
+// fails every other wait and poisons the outputs, so the grid always drains.
 //
 // Reference behaviour restated (mantuoluozk/persistent_lstm_hip): gate order i, f, g, o and the
 // c/h recurrence of persistent_lstm_reference.cpp:21-35; fp16 h storage per step and fp32 c of

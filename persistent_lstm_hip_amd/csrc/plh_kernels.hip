@@ -131,9 +131,6 @@ struct Tile {
 template <int ROWS>
 __device__ __forceinline__ int frag_index(int r, int k) { return ((k >> 3) * ROWS + r) * 8 + (k & 7); }
 
-// The persistent layer-wavefront recurrence.  Template: padded hidden size HP, batch rows per
-// workgroup ROWS (16, or 8 with the MFMA's B columns 8..15 duplicating rows 0..7 so each lane
-// evaluates two (unit, row) pairs instead of four), steps per hand-off chunk CH.
 // a if !sel else b, as one v_cndmask: the empty asm hides that a and b are elements of one vector,
 // which would otherwise be turned into a dynamically indexed extract (three compares and selects).
 __device__ __forceinline__ float pick(bool sel, float a, float b) {
@@ -141,8 +138,11 @@ __device__ __forceinline__ float pick(bool sel, float a, float b) {
   return sel ? b : a;
 }
 
-// RAGGED: rows may end before the tile's last step (lengths given); otherwise every row is live at
-// every step and the state-freezing selects are compiled out.
+// The persistent layer-wavefront recurrence.  Template: padded hidden size HP, batch rows per
+// workgroup ROWS (16, or 8 with the MFMA's B columns 8..15 duplicating rows 0..7 so each lane
+// evaluates two (unit, row) pairs instead of four), steps per hand-off chunk CH, and RAGGED: rows
+// may end before the tile's last step (lengths given); without it every row is live at every step
+// and the state-freezing selects are compiled out.
 template <int HP, int ROWS, int CH, bool RAGGED>
 __global__ void __launch_bounds__(HP / 16 * 64)
 lstm_wavefront_kernel(ForwardArgs a) {

@@ -58,6 +58,7 @@ int capacity(const plh::Geometry& g, int tile_rows, hipError_t* err) {
 struct Plan {
   int tile_rows = 16;
   int chunk_rows = 16;
+  int wg_tiles = 1;  // sliced: 16-row tiles per workgroup
 };
 
 Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
@@ -69,11 +70,18 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
     p.chunk_rows = tiles8 * 8;
     return p;
   }
-  int tiles = cap16 / (g.L * g.slices);
-  if (tiles >= 8) tiles &= ~7;  // keep the XCD-aware mapping available
-  tiles = std::max(1, std::min(tiles, (batch + 15) / 16));
+  // Workgroups per layer of one launch; where the launch is large enough, a multiple of 8 of them
+  // keeps the XCD-aware mapping available.  A sliced workgroup carries two software-pipelined tiles
+  // (where the kernel allows it) only when one tile each would need more than one launch.
+  int groups = cap16 / (g.L * g.slices);
+  if (groups >= 8) groups &= ~7;
+  groups = std::max(1, groups);
+  const int tiles16 = (batch + 15) / 16;
+  const int wt = (g.slices > 1 && g.max_wg_tiles > 1 && tiles16 > groups) ? g.max_wg_tiles : 1;
+  const int tiles = std::min(groups * wt, (tiles16 + wt - 1) / wt * wt);
   p.tile_rows = 16;
   p.chunk_rows = tiles * 16;
+  p.wg_tiles = wt;
   return p;
 }
 
@@ -261,8 +269,10 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     a.row_end = row0 + rows;
     a.tile_rows = plan.tile_rows;
     a.ntile = (rows + plan.tile_rows - 1) / plan.tile_rows;
+    a.wg_tiles = plan.wg_tiles;
+    a.ntile = (a.ntile + a.wg_tiles - 1) / a.wg_tiles * a.wg_tiles;
     a.rows_pad = a.ntile * plan.tile_rows;
-    a.xcd_map = (g.slices > 1 ? (g.L * a.ntile) % 8 : a.ntile % 8) == 0 ? 1 : 0;
+    a.xcd_map = (g.slices > 1 ? (g.L * a.ntile / a.wg_tiles) % 8 : a.ntile % 8) == 0 ? 1 : 0;
     err = plh::launch_zero_u32(counters, (size_t)g.L * a.ntile, s);
     if (err != hipSuccess) return fail_hip(err, "counter reset");
     if (g.slices > 1) {  // tags restart at 1: clear the exchange ring of this launch's tiles

@@ -18,6 +18,7 @@ struct Geometry {
   int I, H, L, O;
   int HP;      // padded hidden size: 32, 64, 128 (one workgroup per layer and tile) or 256, 512 (sliced)
   int slices;  // workgroups per (layer, tile): 1, or HP / 64 (HP = 256) and HP / 32 (HP = 512)
+  int max_wg_tiles;  // 16-row tiles a sliced workgroup can carry (2 at HP = 256, software-pipelined)
   int waves;   // waves per workgroup: HP / 16 (one per 16 hidden units) or 8 when sliced
   int kci;     // input-part K chunks of 32 for layers >= 1 (= HP / 32)
   int kc;      // K chunks of [W_ih | W_hh] per gate row (= 2 * kci)
@@ -82,6 +83,7 @@ struct ForwardArgs {
   int kc_in0;
   int xcd_map;                  // 1: keep a tile's layer chain on one XCD
   uint64_t wait_ticks;          // bound on one inter-workgroup wait, in s_memrealtime ticks (100 MHz)
+  int wg_tiles;                 // sliced kernels: 16-row tiles per workgroup (1 or 2); ntile is a multiple
 };
 
 hipError_t launch_pack_layer(const Geometry& g, int layer, const _Float16* w_ih, const _Float16* w_hh,

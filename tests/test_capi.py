@@ -86,10 +86,11 @@ def test_sliced_workspace_layout(ext):
     # H > 128: the hidden units of a layer are split over several workgroups ("slices").  The workspace
     # holds the (L-1)-layer hand-off plus a two-step ring of tagged words per (layer, tile) through which
     # the slices exchange h every step: L * tiles * 2 * (HP * 8) words of 8 bytes.  Without a device the
-    # plan assumes 256 co-resident workgroups: 256 / (L * 4 slices) = 16 tiles of 16 rows at HP = 256,
-    # and 256 / (L * 16) = 4 tiles at HP = 512.
+    # plan assumes 256 co-resident workgroups: 256 / (L * 4 slices) = 16 workgroups per layer at
+    # HP = 256, each carrying two 16-row tiles (the whole 512-row batch), and 256 / (L * 16) = 4
+    # one-tile workgroups at HP = 512.
     L, T = 4, 1000
-    for H, tiles in ((256, 16), (512, 4)):
+    for H, tiles in ((256, 32), (512, 4)):
         rows = tiles * 16
         b = ext.workspace_bytes(5, H, L, 24, 512, T)
         handoff = (L - 1) * rows * T * H * 2

@@ -358,3 +358,20 @@ def test_sliced_side_stream_and_determinism(gpu):
     gpu.check_status(torch.device("cuda"))
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(a, c)
+
+
+def test_sliced_two_tile_workgroups_ragged_partial_launch(gpu):
+    """H256, 4 layers, 600 rows: one-tile workgroups would need several launches, so each workgroup
+    carries two software-pipelined tiles (512 rows per launch, then 88 rows with a padding tile), with
+    ragged lengths including zeros."""
+    I, H, L, O, B, T = 5, 256, 4, 6, 600, 30
+    _say(f"sliced two-tile ragged B={B}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I, seed=31)
+    lengths = torch.randint(0, T + 1, (B,), generator=torch.Generator().manual_seed(32))
+    model = _gpu_model(native)
+    got = model.forward_ragged(x.to("cuda", torch.float16), lengths)
+    gpu.check_status(torch.device("cuda"))
+    want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
+                                    lengths=lengths.numpy())
+    assert_close(got.float().cpu().numpy(), want, what="two-tile ragged")

@@ -144,12 +144,48 @@ def uniform_batch_protocol(model, dev, warmup: int, steps: int) -> dict:
             "vs_reference_3.08_s": 3.08 / fwd_100}
 
 
+def other_configs(dev, reps: int = 10) -> dict:
+    """C3, C4 and C5 (BASELINE.json configs[2..4]) timed the same way as C2 (HIP events, median of
+    `reps` forwards after 3 warm-ups) on their own synthetic models: parity for these is in
+    tests/test_gpu_parity.py; here only their latency and seq-steps/s are recorded."""
+    from persistent_lstm_hip_amd import PersistentLSTMRegressor, StandardLSTMRegressor
+
+    res = {}
+    for name, hid, ragged in (("C3_H256", 256, False), ("C4_H512", 512, False), ("C5_ragged_H128", 128, True)):
+        torch.manual_seed(42)
+        native = StandardLSTMRegressor(I, hid, O, L).eval()
+        model = PersistentLSTMRegressor.from_native_module(native).to(dev).half().eval()
+        x = torch.randn(B, T, I, generator=torch.Generator().manual_seed(1)).to(dev, torch.float16)
+        lengths = None
+        steps = B * T
+        if ragged:
+            lengths = torch.sort(torch.randint(200, T + 1, (B,), generator=torch.Generator().manual_seed(2)),
+                                 descending=True).values
+            steps = int(lengths.sum())
+        run = (lambda: model.forward_ragged(x, lengths)) if ragged else (lambda: model(x))  # noqa: E731
+        with torch.inference_mode():
+            for _ in range(3):
+                run()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            torch.cuda.synchronize()
+            for a, b in ev:
+                a.record()
+                run()
+                b.record()
+            torch.cuda.synchronize()
+        ms = statistics.median(x0.elapsed_time(x1) for x0, x1 in ev)
+        res[name] = {"latency_s": ms * 1e-3, "seq_steps_per_s": steps / (ms * 1e-3), "hidden": hid,
+                     "lengths": "U[200,1000] sorted descending (Generator seed 2)" if ragged else "all 1000"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100, help="timed forwards")
     ap.add_argument("--warmup", type=int, default=10, help="untimed forwards")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline and parity legs")
+    ap.add_argument("--no-other-configs", action="store_true", help="skip timing C3, C4 and C5")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -193,6 +229,7 @@ def main() -> int:
         ext.kernel_timing(0)
         ext.check_status(dev)
     uniform = uniform_batch_protocol(model, dev, args.warmup, args.steps)
+    others = other_configs(dev) if not args.no_other_configs else None
     total_ms = t_all0.elapsed_time(t_all1)
     per_fwd = sorted(a.elapsed_time(b) for a, b in evs)
     median_ms = statistics.median(per_fwd)
@@ -261,6 +298,7 @@ def main() -> int:
             "latency_ratio": 30.8 / median_ms,
         },
         "uniform_batch": uniform,
+        "other_configs": others,
     }
     if not args.no_cpu_baseline:
         base, cpu_out, rows = cpu_baseline(native, x_cpu)

@@ -284,13 +284,14 @@ def test_sliced_persistent_lstm_dropin_with_state(gpu):
     assert_close(got, want, what="sliced ragged")
 
 
-@pytest.mark.parametrize("H", [128, 256])
-def test_wait_timeout_is_reported_and_recovers(gpu, H):
+@pytest.mark.parametrize("H,B", [(128, 16), (256, 16), (256, 600)])
+def test_wait_timeout_is_reported_and_recovers(gpu, H, B):
     """A forced 1 us wait bound: the next layer's first hand-off wait cannot be met, so the kernel sets
     the timeout status, poisons the outputs and ends; the front end raises; the default bound then
-    gives correct results again (the status word is cleared by every forward)."""
-    I, L, O, B, T = 5, 2, 3, 16, 64
-    _say(f"forced wait timeout H={H}")
+    gives correct results again (the status word is cleared by every forward).  (256, 600) runs the
+    two-tile sliced workgroups."""
+    I, L, O, T = 5, 2, 3, 64
+    _say(f"forced wait timeout H={H} B={B}")
     native = make_regressor(I, H, L, O)
     x = make_x(B, T, I)
     model = _gpu_model(native)

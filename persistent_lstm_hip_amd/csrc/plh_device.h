@@ -1,0 +1,105 @@
+// plh_device.h -- device-side building blocks shared by the gfx950 kernels: vector types, the LSTM
+// cell update, LDS and inter-workgroup synchronisation, the MFMA fragment order, and the work
+// split of the sliced kernels (which their weight packer must reproduce).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "plh_internal.h"
+#include "../../include/persistent_lstm_hip.h"
+
+namespace plh {
+namespace {
+
+typedef f16x8_t f16x8;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// e^{-k z} as 2^(min(-k z log2 e, 40)) on v_exp_f32.  The cap keeps a product of three (1 + e)
+// factors below 2^121 (no overflow) and moves no gate by more than 1e-12 (logistic(-27.7) ~ 1e-12).
+constexpr float kExpCap = 40.0f;
+__device__ __forceinline__ float exp_neg(float z, float k) {
+  return __builtin_amdgcn_exp2f(fminf(z * (-k * kLog2e), kExpCap));
+}
+
+// One LSTM cell update (torch gate order i, f, g, o) from the pre-activations and the old c, with
+// 5 exponentials and 2 reciprocals instead of the 10 transcendentals of evaluating each of
+// sigmoid(i), sigmoid(f), tanh(g), sigmoid(o), tanh(c') as 1 / (1 + e^-x):
+//   c' = sigmoid(f) c + sigmoid(i) tanh(g) = [c (1+ei)(1+eg) + (1-eg)(1+ef)] / [(1+ef)(1+ei)(1+eg)]
+//   h  = sigmoid(o) tanh(c')               = (1 - ec) / [(1+eo)(1+ec)]
+// where ex = e^{-x} for the logistic gates and e^{-2x} for the tanh arguments.  eo alone needs no
+// cap: with ec capped, 1 - ec is finite, so eo = +inf gives h = finite * rcp(inf) = 0, the limit.
+__device__ __forceinline__ void lstm_cell(float zi, float zf, float zg, float zo, float& c, float& h) {
+  const float ei = exp_neg(zi, 1.0f), ef = exp_neg(zf, 1.0f), eg = exp_neg(zg, 2.0f);
+  const float eo = __builtin_amdgcn_exp2f(zo * -kLog2e);
+  const float a = 1.0f + ei, b = 1.0f + eg, d = 1.0f + ef;
+  const float ab = a * b;
+  const float cn = fmaf(c, ab, (1.0f - eg) * d) * __builtin_amdgcn_rcpf(d * ab);
+  const float ec = exp_neg(cn, 2.0f);
+  h = (1.0f - ec) * __builtin_amdgcn_rcpf((1.0f + eo) * (1.0f + ec));
+  c = cn;
+}
+
+// Barrier that orders LDS traffic only: global stores stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Spin (one lane) until *ctr >= need, bounded by `limit` ticks of s_memrealtime (100 MHz), then
+// acquire at agent scope.  Returns 0 if the wait timed out or any workgroup of the grid has failed.
+__device__ int wait_counter(const uint32_t* ctr, uint32_t need, uint32_t* status, uint64_t limit) {
+  uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (v < need) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      __builtin_amdgcn_s_sleep(1);
+      v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (v >= need) break;
+      if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return 0;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
+        __hip_atomic_fetch_or(status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return 0;
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
+}
+
+// Offset (in halfs) of element (row r, k) in a fragment-ordered [ROWS x K] block: the block of K
+// chunk k/32 is stored as [k/8 % 4][row][8], i.e. exactly the B operand of one MFMA.
+template <int ROWS>
+__device__ __forceinline__ int frag_index(int r, int k) { return ((k >> 3) * ROWS + r) * 8 + (k & 7); }
+
+// a if !sel else b, as one v_cndmask: the empty asm hides that a and b are elements of one vector,
+// which would otherwise be turned into a dynamically indexed extract (three compares and selects).
+__device__ __forceinline__ float pick(bool sel, float a, float b) {
+  asm volatile("" : "+v"(b));
+  return sel ? b : a;
+}
+
+// Work split of the sliced kernels (H 129..512): S workgroups ("slices") per (layer, 16-row tile),
+// each holding the gate rows of HS hidden units.
+template <int HP>
+struct Sliced {
+  static constexpr int kKsp = HP / 256;     // waves per K part of a unit group
+  static constexpr int kGroups = 4 / kKsp;  // 16-unit groups per workgroup
+  static constexpr int kHs = 16 * kGroups;  // hidden units per workgroup
+  static constexpr int kS = HP / kHs;       // workgroups per (layer, tile)
+  static constexpr int kKch = HP / 32;      // K chunks of one part
+  static constexpr int kWpg = 2 * kKsp;     // waves per unit group
+  static constexpr int kWords = HP * 8;     // tagged words of one step's h of a 16-row tile
+  // Wave roles: waves 0..3 hold W_ih parts, waves 4..7 W_hh parts, so each SIMD (wave w % 4) runs one
+  // of each and the input waves' MFMAs for step t+1 overlap the recurrent critical path of step t.
+  // Wave w serves unit group (w % 4) / KSP as member e = (w / 4) * KSP + w % KSP of the group
+  // (e < KSP: input part, quarter e; else recurrent part, quarter e - KSP).
+  static __host__ __device__ constexpr int group_of(int w) { return (w & 3) / kKsp; }
+  static __host__ __device__ constexpr int member_of(int w) { return (w >> 2) * kKsp + (w & (kKsp - 1)); }
+  static __host__ __device__ constexpr int wave_of(int g, int e) { return (e / kKsp) * 4 + g * kKsp + e % kKsp; }
+};
+}  // namespace
+}  // namespace plh

@@ -1,4 +1,5 @@
-// plh_internal.h -- declarations shared by the kernels (plh_kernels.hip) and the C ABI (plh_capi.hip).
+// plh_internal.h -- declarations shared by the kernel sources (plh_wavefront.hip, plh_sliced.hip,
+// plh_pack.hip, plh_launch.hip) and the C ABI (plh_capi.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -95,6 +96,12 @@ hipError_t launch_pack_linear(const Geometry& g, const _Float16* w, const _Float
 hipError_t launch_pack_x(const Geometry& g, const ForwardArgs& a, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t s);
 hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, int cols, hipStream_t s);
+
+// Persistent kernels (device function pointers for hipLaunchCooperativeKernel), nullptr if no variant
+// exists: the wavefront kernel for padded H <= 128 and 8- or 16-row tiles (plh_wavefront.hip), the
+// sliced kernel for padded H 256 / 512 with 1 or 2 tiles per workgroup (plh_sliced.hip).
+const void* wavefront_kernel(int HP, int tile_rows, bool ragged);
+const void* sliced_kernel(int HP, int wg_tiles);
 
 // Co-resident workgroups of the persistent kernel on the current device (0 with *err set on error).
 int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err);

@@ -1,0 +1,114 @@
+// plh_launch.hip -- host side of the kernels: geometry rules, buffer layouts, kernel choice,
+// occupancy and the cooperative launch of the persistent recurrence.
+#include "plh_device.h"
+
+namespace plh {
+
+bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
+  if (I <= 0 || H <= 0 || L <= 0 || O < 0) {
+    *why = "input_size, hidden_size and num_layers must be positive and output_size non-negative";
+    return false;
+  }
+  int HP = 0;
+  if (H <= 32) HP = 32;
+  else if (H <= 64) HP = 64;
+  else if (H <= 128) HP = 128;
+  else if (H <= 256) HP = 256;
+  else if (H <= 512) HP = 512;
+  if (HP == 0) {
+    *why = "hidden_size > 512 is not implemented by the persistent kernels";
+    return false;
+  }
+  if (I > HP) {
+    *why = "input_size larger than the padded hidden size is not implemented";
+    return false;
+  }
+  if (L > 64 || O > 4096) {
+    *why = "num_layers > 64 or output_size > 4096 is not implemented";
+    return false;
+  }
+  g->I = I;
+  g->H = H;
+  g->L = L;
+  g->O = O;
+  g->HP = HP;
+  g->slices = HP == 256 ? Sliced<256>::kS : HP == 512 ? Sliced<512>::kS : 1;
+  g->max_wg_tiles = HP == 256 ? 2 : 1;
+  g->waves = g->slices > 1 ? 8 : HP / 16;
+  g->kci = HP / 32;
+  g->kc = 2 * g->kci;
+  g->kc_in0 = (I + 31) / 32;
+  return true;
+}
+
+static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+PackedLayout packed_layout(const Geometry& g) {
+  PackedLayout p;
+  size_t off = 0;
+  p.wpack = off;
+  // HP / 16 gate-row groups x kc chunks of 64 lanes x 8 halfs per gate: the same size whether one
+  // workgroup or `slices` workgroups hold a layer.
+  off = align256(off + (size_t)g.L * (g.HP / 16) * g.kc * 4 * 64 * 8 * sizeof(_Float16));
+  p.bias = off;
+  off = align256(off + (size_t)g.L * 4 * g.HP * sizeof(float));
+  p.wlin = off;
+  off = align256(off + (size_t)g.O * g.HP * sizeof(float));
+  p.blin = off;
+  off = align256(off + (size_t)g.O * sizeof(float));
+  p.total = off;
+  return p;
+}
+
+WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows, int tile_rows) {
+  WorkspaceLayout w;
+  const size_t ntile = (size_t)chunk_rows / tile_rows;
+  const size_t frag_bytes = (size_t)4 * tile_rows * 16;  // one [tile_rows x 32] fp16 fragment block
+  w.chunk_rows = chunk_rows;
+  w.tile_rows = tile_rows;
+  w.status = 0;
+  w.counters = 256;
+  w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile);
+  w.hseq = align256(w.xp + ntile * seq_len * g.kc_in0 * frag_bytes);
+  w.xring = align256(w.hseq + (size_t)(g.L - 1) * ntile * seq_len * g.kci * frag_bytes);
+  w.xring_words = g.slices > 1 ? (size_t)g.L * ntile * 2 * g.HP * 8 : 0;
+  w.total = align256(w.xring + w.xring_words * sizeof(uint64_t));
+  return w;
+}
+
+static const void* recurrent_kernel(const Geometry& g, int tile_rows, bool ragged, int wg_tiles = 1) {
+  if (g.slices > 1) return tile_rows == 16 ? sliced_kernel(g.HP, wg_tiles) : nullptr;
+  return wavefront_kernel(g.HP, tile_rows, ragged);
+}
+
+int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err) {
+  // The smallest occupancy of the variants (with and without lengths, every tile count), so any fits.
+  int cap = 0;
+  for (int v = 0; v < 2 * g.max_wg_tiles; ++v) {
+    const bool ragged = v & 1;
+    const void* fn = recurrent_kernel(g, tile_rows, ragged, 1 + v / 2);
+    if (!fn) {
+      *err = hipErrorInvalidValue;
+      return 0;
+    }
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, g.waves * 64, 0);
+    *err = e;
+    if (e != hipSuccess) return 0;
+    cap = (cap == 0 || per_cu * cus < cap) ? per_cu * cus : cap;
+  }
+  return cap;
+}
+
+hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s) {
+  const void* fn = recurrent_kernel(g, a.tile_rows, a.lengths != nullptr, a.wg_tiles);
+  if (!fn || a.wg_tiles < 1 || a.ntile % a.wg_tiles) return hipErrorInvalidValue;
+  ForwardArgs args = a;
+  void* params[] = {&args};
+  return hipLaunchCooperativeKernel(fn, dim3(a.L * a.ntile / a.wg_tiles * g.slices), dim3(g.waves * 64), params, 0,
+                                    s);
+}
+
+}  // namespace plh

@@ -1,0 +1,189 @@
+// plh_pack.hip -- the layout kernels of the forward: weight packing into per-lane MFMA fragments,
+// x into B-fragment order, and small fills.
+#include "plh_device.h"
+
+namespace plh {
+namespace {
+
+// ---------------------------------------------------------------------------------------------
+// Weight packing: torch layout -> per-lane MFMA A fragments.
+// For 16x16x32 f16, lane l of the A operand holds A[m = l % 16][k = 8 * (l / 16) + j], j < 8.
+// Row m of tile (wave w, gate q) is gate column q*H + w*16 + m; K runs over [x | h] in chunks
+// of 32: chunks [0, kci) index W_ih columns, [kci, kc) index W_hh columns; out-of-range -> 0.
+template <int HP>
+__global__ void pack_layer_kernel(const _Float16* __restrict__ w_ih, const _Float16* __restrict__ w_hh, int K,
+                                  int H, _Float16* __restrict__ dst) {
+  constexpr int kWaves = HP / 16, kKci = HP / 32, kKc = 2 * kKci;
+  const size_t total = (size_t)kWaves * kKc * 4 * 64 * 8;
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= total) return;
+  const int j = e & 7;
+  const int lane = (e >> 3) & 63;
+  const int q = (e >> 9) & 3;
+  const int kc = (int)((e >> 11) % kKc);
+  const int wv = (int)((e >> 11) / kKc);
+  const int m = lane & 15, kgrp = lane >> 4;
+  const int u = wv * 16 + m;
+  const size_t col = (size_t)q * H + u;
+  _Float16 v = (_Float16)0.0f;
+  if (u < H) {
+    if (kc < kKci) {
+      const int k = kc * 32 + kgrp * 8 + j;
+      if (k < K) v = w_ih[col * K + k];
+    } else {
+      const int k = (kc - kKci) * 32 + kgrp * 8 + j;
+      if (k < H) v = w_hh[col * H + k];
+    }
+  }
+  dst[e] = v;
+}
+
+// Sliced weights: [L][S][8 waves][8 chunks][4 gates][64 lanes][8].  Wave w of slice s holds unit
+// group Sliced::group_of(w); member e = Sliced::member_of(w) selects the part e / KSP (0: W_ih,
+// 1: W_hh) and the quarter e % KSP of that part's columns.
+template <int HP>
+__global__ void pack_sliced_kernel(const _Float16* __restrict__ w_ih, const _Float16* __restrict__ w_hh, int K,
+                                   int H, _Float16* __restrict__ dst) {
+  using C = Sliced<HP>;
+  const size_t total = (size_t)C::kS * 8 * 8 * 4 * 64 * 8;
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= total) return;
+  const int j = e & 7;
+  const int lane = (e >> 3) & 63;
+  const int q = (e >> 9) & 3;
+  const int kc = (int)((e >> 11) & 7);
+  const int wv = (int)((e >> 14) & 7);
+  const int sl = (int)(e >> 17);
+  const int g = C::group_of(wv), ew = C::member_of(wv);
+  const bool rec = ew >= C::kKsp;
+  const int kq = ew % C::kKsp;
+  const int u = sl * C::kHs + g * 16 + (lane & 15);
+  const size_t col = (size_t)q * H + u;
+  const int k = (kq * 8 + kc) * 32 + (lane >> 4) * 8 + j;
+  _Float16 v = (_Float16)0.0f;
+  if (u < H) {
+    if (!rec) {
+      if (k < K) v = w_ih[col * K + k];
+    } else {
+      if (k < H) v = w_hh[col * H + k];
+    }
+  }
+  dst[e] = v;
+}
+
+__global__ void pack_bias_kernel(const _Float16* __restrict__ b_ih, const _Float16* __restrict__ b_hh, int H, int HP,
+                                 float* __restrict__ dst) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= 4 * HP) return;
+  const int q = e / HP, u = e % HP;
+  float v = 0.0f;
+  if (u < H) {
+    if (b_ih) v += (float)b_ih[q * H + u];
+    if (b_hh) v += (float)b_hh[q * H + u];
+  }
+  dst[e] = v;
+}
+
+__global__ void pack_linear_kernel(const _Float16* __restrict__ w, const _Float16* __restrict__ b, int O, int H,
+                                   int HP, float* __restrict__ wl, float* __restrict__ bl) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < O * HP) {
+    const int o = e / HP, k = e % HP;
+    wl[e] = k < H ? (float)w[(size_t)o * H + k] : 0.0f;
+  }
+  if (e < O) bl[e] = b ? (float)b[e] : 0.0f;
+}
+
+// x [B, T, I] -> xp [ntile][T][kci0][4][rows] f16x8: B-fragment order for tiles of `rows` rows,
+// zero padded.
+__global__ void pack_x_kernel(const _Float16* __restrict__ x, int T, int I, int row0, int row_end, int ntile,
+                              int rows, int kci0, f16x8* __restrict__ xp) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int fv = 4 * rows;
+  const size_t total = (size_t)ntile * T * kci0 * fv;
+  if (e >= total) return;
+  const int f = (int)(e % fv);
+  const int kc = (int)((e / fv) % kci0);
+  const size_t tt = e / ((size_t)fv * kci0);
+  const int t = (int)(tt % T);
+  const int tile = (int)(tt / T);
+  const int b = row0 + tile * rows + f % rows;
+  const int k0 = kc * 32 + (f / rows) * 8;
+  f16x8 v = {};
+  if (b < row_end) {
+    const _Float16* src = x + ((size_t)b * T + t) * I;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (k0 + j < I) v[j] = src[k0 + j];
+  }
+  xp[e] = v;
+}
+
+__global__ void zero_u32_kernel(uint32_t* __restrict__ p, size_t n) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < n) p[e] = 0u;
+}
+
+__global__ void repeat_first_row_kernel(const _Float16* __restrict__ in, _Float16* __restrict__ out, int rows, int cols) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < (size_t)rows * cols) out[e] = in[e % cols];
+}
+
+inline unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+hipError_t launch_pack_layer(const Geometry& g, int layer, const _Float16* w_ih, const _Float16* w_hh, _Float16* wpack,
+                             hipStream_t s) {
+  const size_t per_layer = (size_t)(g.HP / 16) * g.kc * 4 * 64 * 8;
+  _Float16* dst = wpack + per_layer * layer;
+  const int K = layer == 0 ? g.I : g.H;
+  const unsigned grid = blocks_for(per_layer, 256);
+  switch (g.HP) {
+    case 32: hipLaunchKernelGGL(pack_layer_kernel<32>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
+    case 64: hipLaunchKernelGGL(pack_layer_kernel<64>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
+    case 128: hipLaunchKernelGGL(pack_layer_kernel<128>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
+    case 256: hipLaunchKernelGGL(pack_sliced_kernel<256>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
+    case 512: hipLaunchKernelGGL(pack_sliced_kernel<512>, grid, 256, 0, s, w_ih, w_hh, K, g.H, dst); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_bias(const Geometry& g, int layer, const _Float16* b_ih, const _Float16* b_hh, float* bias,
+                            hipStream_t s) {
+  hipLaunchKernelGGL(pack_bias_kernel, blocks_for(4 * g.HP, 256), 256, 0, s, b_ih, b_hh, g.H, g.HP,
+                     bias + (size_t)layer * 4 * g.HP);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_linear(const Geometry& g, const _Float16* w, const _Float16* b, float* wlin, float* blin,
+                              hipStream_t s) {
+  if (g.O == 0) return hipSuccess;
+  hipLaunchKernelGGL(pack_linear_kernel, blocks_for((size_t)g.O * g.HP, 256), 256, 0, s, w, b, g.O, g.H, g.HP, wlin,
+                     blin);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_x(const Geometry& g, const ForwardArgs& a, hipStream_t s) {
+  const size_t n = (size_t)a.ntile * a.T * g.kc_in0 * 4 * a.tile_rows;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(pack_x_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, a.I, a.row0, a.row_end, a.ntile,
+                     a.tile_rows, g.kc_in0, a.xp);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_u32_kernel, blocks_for(n, 256), 256, 0, s, p, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, int cols, hipStream_t s) {
+  const size_t n = (size_t)rows * cols;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(repeat_first_row_kernel, blocks_for(n, 256), 256, 0, s, in, out, rows, cols);
+  return hipGetLastError();
+}
+
+}  // namespace plh

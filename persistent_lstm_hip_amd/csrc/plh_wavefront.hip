@@ -1,0 +1,431 @@
+// plh_wavefront.hip -- the persistent layer-wavefront kernel (H <= 128) of the stacked LSTM +
+// Linear inference forward on CDNA4 (gfx950).  Cooperative launch: every workgroup is co-resident
+// and loops over the time steps itself.
+//
+// One workgroup per (layer, batch tile of 8 or 16 rows):
+//   * each wave owns 16 hidden units and keeps the i, f, g, o rows of [W_ih | W_hh] for them in
+//     VGPRs for the whole sequence as fp16 MFMA A fragments (256 KB per layer at H = 128);
+//   * per step a wave computes gates^T[64 gate cols, 16 cols] = W[64, K] * [in_t | h_{t-1}]^T with
+//     v_mfma_f32_16x16x32_f16 (fp32 accumulate, bias as the initial accumulator); with 8-row tiles
+//     the B columns 8..15 repeat rows 0..7 and each lane evaluates two of its four (unit, row)
+//     pairs; the next step's input part is issued between this step's gate computations;
+//   * the gate nonlinearities and the c/h update run on the accumulator registers; c never leaves
+//     VGPRs; h goes to an LDS history ring that also feeds the next step's recurrent MFMAs;
+//   * activations live in "fragment order": a [R rows x 32 k] block is stored as [k/8][row][8],
+//     i.e. exactly the B operand of one MFMA (lane l reads 16 B at l * 16), in LDS and in the
+//     global hand-off buffer, so LDS traffic is conflict-free and global traffic contiguous;
+//   * the step input (x for layer 0, h of layer l-1 otherwise) reaches LDS one chunk of CH steps at
+//     a time, loaded to VGPRs during the previous chunk, so no step waits on global memory;
+//   * the hand-off between layers is a per-(layer, tile) step counter published with an agent-scope
+//     release once per chunk and observed with a deferred poll + agent-scope acquire one chunk
+//     ahead: layer l+1 works on chunk k while layer l works on later chunks;
+//   * the Linear head runs in the last layer's epilogue on the final h held in LDS;
+//   * every wait between workgroups is bounded in wall-clock time; a failed wait sets a status bit,
+//     fails every other wait and poisons the outputs, so the grid always drains.
+//
+// Reference behaviour restated (mantuoluozk/persistent_lstm_hip): gate order i, f, g, o and the
+// c/h recurrence of persistent_lstm_reference.cpp:21-35; fp16 h storage per step and fp32 c of
+// persistent_lstm_hip.cu:520-525; the fp32-accumulated head of persistent_lstm_hip.cu:1662-1682.
+#include "plh_device.h"
+
+namespace plh {
+namespace {
+
+// Workgroup -> (layer, tile).  With xcd_map, workgroups are dispatched round-robin over the 8
+// XCDs (block b lands on XCD b % 8), and the mapping puts all layers of a tile on one XCD.
+__device__ __forceinline__ void block_coords(int b, int ntile, int xcd_map, int& layer, int& tile) {
+  if (xcd_map) {
+    const int per = ntile >> 3;
+    const int r = b >> 3;
+    tile = (b & 7) * per + r % per;
+    layer = r / per;
+  } else {
+    layer = b / ntile;
+    tile = b % ntile;
+  }
+}
+
+template <int HP, int ROWS, int CH>
+struct Tile {
+  static_assert(ROWS == 8 || ROWS == 16, "tiles hold 8 or 16 batch rows");
+  static constexpr int kWaves = HP / 16;
+  static constexpr int kThreads = kWaves * 64;
+  static constexpr int kKci = HP / 32;          // input-part K chunks (layers >= 1)
+  static constexpr int kKcr = HP / 32;          // recurrent K chunks
+  static constexpr int kKc = kKci + kKcr;
+  static constexpr int kFragVec = 4 * ROWS;     // f16x8 per [ROWS x 32] fragment block
+  static constexpr int kUpl = ROWS / 4;         // (unit, row) pairs per lane in the epilogue
+  // f16x8 elements each thread moves per chunk (input ring fill, hand-off copy)
+  static constexpr int kRn = (CH * kKci * kFragVec + kThreads - 1) / kThreads;
+};
+
+// The persistent layer-wavefront recurrence.  Template: padded hidden size HP, batch rows per
+// workgroup ROWS (16, or 8 with the MFMA's B columns 8..15 duplicating rows 0..7 so each lane
+// evaluates two (unit, row) pairs instead of four), steps per hand-off chunk CH, and RAGGED: rows
+// may end before the tile's last step (lengths given); without it every row is live at every step
+// and the state-freezing selects are compiled out.
+template <int HP, int ROWS, int CH, bool RAGGED>
+__global__ void __launch_bounds__(HP / 16 * 64)
+lstm_wavefront_kernel(ForwardArgs a) {
+  using C = Tile<HP, ROWS, CH>;
+  constexpr int KCI = C::kKci, KCR = C::kKcr, KC = C::kKc, NT = C::kThreads, FV = C::kFragVec;
+  constexpr int UPL = C::kUpl, RN = C::kRn;
+
+  __shared__ f16x8 ring[CH * KCI * FV];   // step inputs of the current chunk
+  __shared__ f16x8 hist[CH * KCR * FV];   // h of the chunk's steps; slot (t-1) % CH feeds step t
+  __shared__ int s_ok[2];
+  __shared__ int s_tlen;
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;            // B-operand / D column
+  const int kg = lane >> 4;           // K group of the A/B fragments, row group of D
+  const int r = n & (ROWS - 1);       // batch row in the tile
+  const int fl = kg * ROWS + r;       // this lane's B fragment within a block
+  int layer, tile;
+  block_coords(blockIdx.x, a.ntile, a.xcd_map, layer, tile);
+
+  const int grow = a.row0 + tile * ROWS + r;
+  const bool row_ok = grow < a.row_end;
+  int len = 0;
+  if (row_ok) {
+    len = a.lengths ? a.lengths[grow] : a.T;
+    len = len < 0 ? 0 : (len > a.T ? a.T : len);
+  }
+  if (threadIdx.x == 0) s_tlen = 0;
+  __syncthreads();
+  if (wave == 0 && kg == 0) atomicMax(&s_tlen, len);
+  __syncthreads();
+  const int Tt = s_tlen;  // steps this tile runs: the longest row in it
+
+  // Resident weights: A fragments of [W_ih | W_hh] rows for this wave's 16 units, 4 gates.
+  f16x8 w[KC][4];
+  {
+    const f16x8* wp = reinterpret_cast<const f16x8*>(a.wpack) + ((size_t)(layer * C::kWaves + wave) * KC * 4) * 64 + lane;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
+  }
+  // D rows of this lane: units u0 .. u0+3 of row n; it evaluates UPL of them, starting at uo.
+  const int u0 = wave * 16 + kg * 4;
+  const int ibase = (ROWS == 8 && n >= 8) ? 2 : 0;
+  const int uo = u0 + ibase;
+  f32x4 bias[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) bias[q] = *reinterpret_cast<const f32x4*>(a.bias + ((size_t)layer * 4 + q) * HP + u0);
+
+  // Initial state (nn.LSTM hx) or zeros; h_{-1} goes to history slot CH-1.
+  typedef _Float16 hvec __attribute__((ext_vector_type(UPL)));
+  float c[UPL];
+  hvec hcur;
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = uo + j;
+    const bool v = row_ok && u < a.H;
+    const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
+    c[j] = (v && a.c0) ? (float)a.c0[si] : 0.0f;
+    hcur[j] = (v && a.h0) ? a.h0[si] : (_Float16)0.0f;
+  }
+  const int hoff = frag_index<ROWS>(r, uo);  // where this lane's UPL h values go (contiguous)
+  auto hist_h = [&](int slot) -> _Float16* { return reinterpret_cast<_Float16*>(hist + slot * (KCR * FV)) + hoff; };
+  *reinterpret_cast<hvec*>(hist_h(CH - 1)) = hcur;
+
+  const bool has_up = layer > 0;
+  const bool has_down = layer < a.L - 1;
+  const int kin = has_up ? KCI : a.kc_in0;  // input fragment blocks per step
+  const size_t hstep = (size_t)KCR * FV;     // f16x8 per (tile, step) in the hand-off buffer
+  const f16x8* in_seq = has_up ? a.hseq + ((size_t)(layer - 1) * a.ntile + tile) * a.T * hstep
+                               : a.xp + (size_t)tile * a.T * kin * FV;
+  f16x8* out_seq_h = has_down ? a.hseq + ((size_t)layer * a.ntile + tile) * a.T * hstep : nullptr;
+  const uint32_t* up_ctr = has_up ? a.counters + (layer - 1) * a.ntile + tile : nullptr;
+  uint32_t* my_ctr = a.counters + layer * a.ntile + tile;
+  const int sync_tid = C::kWaves > 1 ? 64 : 0;  // the lane that polls upstream (wave 1)
+
+  const int nchunk = (Tt + CH - 1) / CH;
+  f16x8 R[RN];
+  auto load_chunk = [&](int k) {
+    const int s0 = k * CH;
+    const int nel = min(CH, Tt - s0) * kin * FV;
+    const f16x8* src = in_seq + (size_t)s0 * kin * FV;
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < nel) R[i] = src[idx];
+    }
+  };
+  // The ring always holds KCI fragment blocks per step; layer 0 fills the first kin of them (the
+  // others stay zero from the initialisation), so every layer runs the same branch-free MFMAs.
+  auto store_chunk = [&](int k) {
+    const int per = kin * FV;
+    const int nel = min(CH, Tt - k * CH) * per;
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < nel) ring[(idx / per) * (KCI * FV) + idx % per] = R[i];
+    }
+  };
+  // Hand-off copy of chunk k's h history (LDS) to the global sequence buffer.
+  auto copy_out = [&](int k) {
+    const int nel = min(CH, Tt - k * CH) * (KCR * FV);
+    f16x8* dst = out_seq_h + (size_t)k * CH * hstep;
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < nel) dst[idx] = hist[idx];
+    }
+  };
+  auto need_for = [&](int k) -> uint32_t { return (uint32_t)min((k + 1) * CH, Tt); };  // chunk k published
+
+  int wait_idx = 0;
+  auto wait_up = [&](uint32_t need) -> bool {  // blocking wait for the upstream layer
+    const int slot = wait_idx++ & 1;
+    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(up_ctr, need, a.status, a.wait_ticks);
+    __syncthreads();
+    return s_ok[slot] != 0;
+  };
+
+  int probe_i = 0;
+  int probe_next = a.n_probe > 0 ? a.probe_steps[0] : -1;
+  auto write_probe = [&](int p) {
+    if (!row_ok) return;
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+      const int u = uo + j;
+      if (u < a.H) {
+        const size_t o = (((size_t)p * a.L + layer) * a.B + grow) * a.H + u;
+        a.probe_h[o] = (float)hcur[j];
+        a.probe_c[o] = c[j];
+      }
+    }
+  };
+
+  for (int i = threadIdx.x; i < CH * KCI * FV; i += NT) ring[i] = f16x8{};
+  __syncthreads();
+
+  bool ok = true;
+  uint32_t poll = 0;  // deferred observation of the upstream counter (sync_tid only)
+  if (Tt > 0) {
+    if (has_up) ok = wait_up(need_for(0));
+    if (ok) {
+      load_chunk(0);
+      store_chunk(0);
+    }
+    if (ok && nchunk > 1) {
+      if (has_up) ok = wait_up(need_for(1));
+      if (ok) load_chunk(1);
+    }
+    if (has_up && threadIdx.x == sync_tid) poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();  // ring (chunk 0) and the initial h visible
+
+  const bool hi = ibase != 0;
+  for (int k = 0; ok && k < nchunk; ++k) {
+    if (k > 0) {
+      // Chunk boundary: hand chunk k-1's h to global memory, move chunk k's input from VGPRs into
+      // the ring, acquire chunk k+1 of the upstream layer and start loading it.
+      __syncthreads();
+      if (has_down) copy_out(k - 1);
+      store_chunk(k);
+      const bool more = k + 1 < nchunk;
+      const int slot = wait_idx++ & 1;
+      if (has_up && more && threadIdx.x == sync_tid) {
+        const uint32_t need = need_for(k + 1);
+        int okv;
+        if (poll >= need) {
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          okv = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
+        } else {
+          okv = wait_counter(up_ctr, need, a.status, a.wait_ticks);
+        }
+        poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_ok[slot] = okv;
+      }
+      __syncthreads();  // also orders every wave's hand-off stores before the publication below
+      if (has_up && more && s_ok[slot] == 0) {
+        ok = false;
+        break;
+      }
+      if (more) load_chunk(k + 1);
+    }
+
+    const int ns = min(CH, Tt - k * CH);
+    // Chunk k-1 is published halfway through chunk k: its stores have drained by then, so the
+    // release costs the publishing wave little.
+    const int pub_s = (k > 0 && has_down) ? min(CH / 2, ns - 1) : -1;
+    f32x4 acc_next[4];
+    {
+      const f16x8* xr = ring + fl;
+      f16x8 xv[KCI];
+#pragma unroll
+      for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
+#pragma unroll
+      for (int kc = 0; kc < KCI; ++kc)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
+    }
+    for (int s = 0; s < ns; ++s) {
+      const int t = k * CH + s;
+      f32x4 acc[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = acc_next[q];
+      // Recurrent part: h_{t-1} from the history slot of the previous step.
+      const f16x8* hr = hist + (s == 0 ? CH - 1 : s - 1) * (KCR * FV) + fl;
+      f16x8 hv[KCR];
+#pragma unroll
+      for (int kr = 0; kr < KCR; ++kr) hv[kr] = hr[kr * FV];
+#pragma unroll
+      for (int kr = 0; kr < KCR; ++kr)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[KCI + kr][q], hv[kr], acc[q], 0, 0, 0);
+
+      // Next step's input part (the chunk's last step recomputes a discarded in-range step),
+      // interleaved with this step's gate math: each (unit, row) piece of the epilogue is preceded
+      // by its share of the next step's MFMAs and fenced with sched_barrier, so the matrix core
+      // runs while the VALU evaluates the gates (in-order issue would otherwise queue all VALU
+      // work behind the MFMAs).
+      const f16x8* xr = ring + min(s + 1, ns - 1) * (KCI * FV) + fl;
+      f16x8 xv[KCI];
+#pragma unroll
+      for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
+      const bool live = t < len;
+      constexpr int kMfmaPerPiece = (KCI * 4 + UPL - 1) / UPL;
+#pragma unroll
+      for (int j = 0; j < UPL; ++j) {
+#pragma unroll
+        for (int m = j * kMfmaPerPiece; m < (j + 1) * kMfmaPerPiece && m < KCI * 4; ++m) {
+          const int kc = m / 4, q = m % 4;
+          acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
+        }
+        // this lane's pair j: D element ibase + j of every gate tile (one v_cndmask each)
+        float z[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) z[q] = pick(hi, acc[q][j], acc[q][2 + j % 2]);
+        float cn = c[j], hn;
+        lstm_cell(z[0], z[1], z[2], z[3], cn, hn);
+        if constexpr (RAGGED) {
+          // selects, not a branch: rows past their length keep their state
+          c[j] = live ? cn : c[j];
+          hcur[j] = live ? (_Float16)hn : hcur[j];
+        } else {
+          c[j] = cn;
+          hcur[j] = (_Float16)hn;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      *reinterpret_cast<hvec*>(hist_h(s)) = hcur;
+      if (!has_down && a.out_seq && row_ok) {
+        _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
+#pragma unroll
+        for (int j = 0; j < UPL; ++j)
+          if (uo + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
+      }
+      if (t + 1 == probe_next) {
+        write_probe(probe_i);
+        ++probe_i;
+        probe_next = probe_i < a.n_probe ? a.probe_steps[probe_i] : -1;
+      }
+      if (s == pub_s && threadIdx.x == 0)
+        __hip_atomic_store(my_ctr, (uint32_t)(k * CH), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      lds_barrier();
+    }
+  }
+
+  if (!ok) {
+    // A hand-off wait failed (the status word records it and fails every other wait): poison this
+    // tile's head outputs and leave.
+    if (!has_down && a.out) {
+      for (int idx = threadIdx.x; idx < ROWS * a.O; idx += NT) {
+        const int g = a.row0 + tile * ROWS + idx / a.O;
+        if (g < a.row_end) a.out[(size_t)g * a.O + idx % a.O] = (_Float16)__builtin_nanf("");
+      }
+    }
+    return;
+  }
+  if (has_down && Tt > 0) {
+    __syncthreads();
+    copy_out(nchunk - 1);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(my_ctr, (uint32_t)Tt, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // Steps past the tile's longest row were never visited: their output sequence is zero.
+  if (!has_down && a.out_seq && row_ok) {
+    for (int t = Tt; t < a.T; ++t) {
+      _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
+#pragma unroll
+      for (int j = 0; j < UPL; ++j)
+        if (uo + j < a.H) dst[j] = (_Float16)0.0f;
+    }
+  }
+
+  // States after the tile's last step (rows that ended earlier were frozen at their last step).
+  while (probe_i < a.n_probe) {
+    write_probe(probe_i);
+    ++probe_i;
+  }
+  if (row_ok) {
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+      const int u = uo + j;
+      if (u < a.H) {
+        const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
+        if (a.h_n) a.h_n[si] = hcur[j];
+        if (a.c_n) a.c_n[si] = (_Float16)c[j];
+      }
+    }
+  }
+
+  // Linear head on the final h of the last layer (history slot of the tile's last step).
+  if (!has_down && a.out) {
+    const _Float16* hf = reinterpret_cast<const _Float16*>(hist + ((Tt + CH - 1) % CH) * (KCR * FV));
+    for (int idx = threadIdx.x; idx < ROWS * a.O; idx += NT) {
+      const int rr = idx / a.O, o = idx % a.O;
+      const int g = a.row0 + tile * ROWS + rr;
+      if (g >= a.row_end) continue;
+      const float* wr = a.wlin + (size_t)o * HP;
+      float s0 = 0.f, s1 = 0.f;
+      for (int k8 = 0; k8 < HP; k8 += 8) {
+        const f16x8 hv = *reinterpret_cast<const f16x8*>(hf + frag_index<ROWS>(rr, k8));
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          s0 = fmaf((float)hv[j], wr[k8 + j], s0);
+          s1 = fmaf((float)hv[j + 1], wr[k8 + j + 1], s1);
+        }
+      }
+      a.out[(size_t)g * a.O + o] = (_Float16)(a.blin[o] + (s0 + s1));
+    }
+  }
+}
+
+}  // namespace
+
+// Steps per hand-off chunk (compile-time tuning knob).
+#ifndef PLH_CHUNK_STEPS
+#define PLH_CHUNK_STEPS 8
+#endif
+constexpr int kChunk = PLH_CHUNK_STEPS;
+
+template <int ROWS, bool RAGGED>
+static const void* wavefront_kernel_rows(int HP) {
+  switch (HP) {
+    case 32: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<32, ROWS, kChunk, RAGGED>);
+    case 64: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<64, ROWS, kChunk, RAGGED>);
+    case 128: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<128, ROWS, kChunk, RAGGED>);
+    default: return nullptr;
+  }
+}
+
+const void* wavefront_kernel(int HP, int tile_rows, bool ragged) {
+  if (tile_rows == 8) return ragged ? wavefront_kernel_rows<8, true>(HP) : wavefront_kernel_rows<8, false>(HP);
+  if (tile_rows == 16) return ragged ? wavefront_kernel_rows<16, true>(HP) : wavefront_kernel_rows<16, false>(HP);
+  return nullptr;
+}
+
+}  // namespace plh

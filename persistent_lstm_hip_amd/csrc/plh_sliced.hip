@@ -370,7 +370,9 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   };
 
   int probe_i = 0;
-  int probe_next = a.n_probe > 0 ? a.probe_steps[0] : -1;
+  // Probe steps live in SGPRs (see the wavefront kernel): a VGPR loaded in the loop would put a
+  // vmcnt(0) on every step.
+  int probe_next = a.n_probe > 0 ? __builtin_amdgcn_readfirstlane(a.probe_steps[0]) : -1;
   auto write_probe = [&](int pi) {
     if (!active) return;
 #pragma unroll
@@ -466,7 +468,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       if (t + 1 == probe_next) {
         write_probe(probe_i);
         ++probe_i;
-        probe_next = probe_i < a.n_probe ? a.probe_steps[probe_i] : -1;
+        probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
       }
       ++unpublished;
     }

@@ -186,7 +186,10 @@ lstm_wavefront_kernel(ForwardArgs a) {
   };
 
   int probe_i = 0;
-  int probe_next = a.n_probe > 0 ? a.probe_steps[0] : -1;
+  // Probe steps are wave-uniform and kept in SGPRs (readfirstlane right after the load): a VGPR
+  // loaded in the loop would make the compiler wait for every outstanding global access (vmcnt(0),
+  // in order on gfx950, so the chunk prefetch and the hand-off stores included) at each step.
+  int probe_next = a.n_probe > 0 ? __builtin_amdgcn_readfirstlane(a.probe_steps[0]) : -1;
   auto write_probe = [&](int p) {
     if (!row_ok) return;
 #pragma unroll
@@ -329,7 +332,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
       if (t + 1 == probe_next) {
         write_probe(probe_i);
         ++probe_i;
-        probe_next = probe_i < a.n_probe ? a.probe_steps[probe_i] : -1;
+        probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
       }
       if (s == pub_s && threadIdx.x == 0)
         __hip_atomic_store(my_ctr, (uint32_t)(k * CH), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);

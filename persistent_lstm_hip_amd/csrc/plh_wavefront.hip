@@ -15,10 +15,14 @@
 //     i.e. exactly the B operand of one MFMA (lane l reads 16 B at l * 16), in LDS and in the
 //     global hand-off buffer, so LDS traffic is conflict-free and global traffic contiguous;
 //   * the step input (x for layer 0, h of layer l-1 otherwise) reaches LDS one chunk of CH steps at
-//     a time, loaded to VGPRs during the previous chunk, so no step waits on global memory;
-//   * the hand-off between layers is a per-(layer, tile) step counter published with an agent-scope
-//     release once per chunk and observed with a deferred poll + agent-scope acquire one chunk
-//     ahead: layer l+1 works on chunk k while layer l works on later chunks;
+//     a time into a double-buffered ring, loaded four steps before it is needed, so no step waits
+//     on global memory;
+//   * the hand-off between layers is a per-(layer, tile) step counter: the h of each chunk goes to
+//     the hand-off buffer with agent-scope (sc1) stores, and once every wave's stores completed the
+//     counter is advanced with a relaxed store (no L2 write-back); the next layer polls it and reads
+//     the chunk after an agent-scope acquire.  All per-chunk work sits on fixed steps of the chunk
+//     (the step body is inlined per step), so there is no chunk-boundary barrier and layer l+1 runs
+//     about two chunks behind layer l;
 //   * the Linear head runs in the last layer's epilogue on the final h held in LDS;
 //   * every wait between workgroups is bounded in wall-clock time; a failed wait sets a status bit,
 //     fails every other wait and poisons the outputs, so the grid always drains.
@@ -70,10 +74,15 @@ lstm_wavefront_kernel(ForwardArgs a) {
   using C = Tile<HP, ROWS, CH>;
   constexpr int KCI = C::kKci, KCR = C::kKcr, KC = C::kKc, NT = C::kThreads, FV = C::kFragVec;
   constexpr int UPL = C::kUpl, RN = C::kRn;
+  static_assert(CH >= 4 && (CH & (CH - 1)) == 0, "the hand-off schedule needs a power-of-two chunk of >= 4 steps");
+  constexpr int kRingBuf = CH * KCI * FV;  // f16x8 per ring buffer (one chunk of step inputs)
+  constexpr int kHistBuf = CH * KCR * FV;  // f16x8 per history buffer (one chunk of h)
 
-  __shared__ f16x8 ring[CH * KCI * FV];   // step inputs of the current chunk
-  __shared__ f16x8 hist[CH * KCR * FV];   // h of the chunk's steps; slot (t-1) % CH feeds step t
-  __shared__ int s_ok[2];
+  // Both are double-buffered by chunk parity, so chunk k+1's inputs can be written and chunk k-1's
+  // h copied out while chunk k runs.
+  __shared__ f16x8 ring[2 * kRingBuf];  // step inputs: chunk k in buffer k & 1
+  __shared__ f16x8 hist[2 * kHistBuf];  // h of every step: step (k, s) in buffer k & 1, slot s
+  __shared__ int s_ok;
   __shared__ int s_tlen;
 
   const int wave = threadIdx.x >> 6;
@@ -115,7 +124,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) bias[q] = *reinterpret_cast<const f32x4*>(a.bias + ((size_t)layer * 4 + q) * HP + u0);
 
-  // Initial state (nn.LSTM hx) or zeros; h_{-1} goes to history slot CH-1.
+  // Initial state (nn.LSTM hx) or zeros; h_{-1} is step CH-1 of "chunk -1" (history buffer 1).
   typedef _Float16 hvec __attribute__((ext_vector_type(UPL)));
   float c[UPL];
   hvec hcur;
@@ -128,8 +137,10 @@ lstm_wavefront_kernel(ForwardArgs a) {
     hcur[j] = (v && a.h0) ? a.h0[si] : (_Float16)0.0f;
   }
   const int hoff = frag_index<ROWS>(r, uo);  // where this lane's UPL h values go (contiguous)
-  auto hist_h = [&](int slot) -> _Float16* { return reinterpret_cast<_Float16*>(hist + slot * (KCR * FV)) + hoff; };
-  *reinterpret_cast<hvec*>(hist_h(CH - 1)) = hcur;
+  auto hist_h = [&](int t) -> _Float16* {
+    return reinterpret_cast<_Float16*>(hist + ((t / CH) & 1) * kHistBuf + (t % CH) * (KCR * FV)) + hoff;
+  };
+  *reinterpret_cast<hvec*>(hist_h(2 * CH - 1)) = hcur;
 
   const bool has_up = layer > 0;
   const bool has_down = layer < a.L - 1;
@@ -143,52 +154,57 @@ lstm_wavefront_kernel(ForwardArgs a) {
   const int sync_tid = C::kWaves > 1 ? 64 : 0;  // the lane that polls upstream (wave 1)
 
   const int nchunk = (Tt + CH - 1) / CH;
+  // Chunk k's step inputs: loaded into VGPRs (R) 4 steps before they are needed, written to ring
+  // buffer k & 1 at step CH - 2.  Every lane loads (indices clamped into the chunk), so the loads
+  // write R directly; positions that hold no data are not written (layer 0 fills the first kin
+  // fragment blocks of a step, the rest stay zero from the initialisation).
   f16x8 R[RN];
   auto load_chunk = [&](int k) {
-    const int s0 = k * CH;
-    const int nel = min(CH, Tt - s0) * kin * FV;
-    const f16x8* src = in_seq + (size_t)s0 * kin * FV;
+    const int ns_k = min(CH, Tt - k * CH);
+    const f16x8* src = in_seq + (size_t)k * CH * kin * FV;
 #pragma unroll
     for (int i = 0; i < RN; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      if (idx < nel) R[i] = src[idx];
+      const int p = (int)threadIdx.x + i * NT;
+      const int st = min(p / (KCI * FV), ns_k - 1), e = min(p % (KCI * FV), kin * FV - 1);
+      R[i] = src[st * kin * FV + e];
     }
   };
-  // The ring always holds KCI fragment blocks per step; layer 0 fills the first kin of them (the
-  // others stay zero from the initialisation), so every layer runs the same branch-free MFMAs.
   auto store_chunk = [&](int k) {
-    const int per = kin * FV;
-    const int nel = min(CH, Tt - k * CH) * per;
+    const int ns_k = min(CH, Tt - k * CH);
+    f16x8* rb = ring + (k & 1) * kRingBuf;
 #pragma unroll
     for (int i = 0; i < RN; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      if (idx < nel) ring[(idx / per) * (KCI * FV) + idx % per] = R[i];
+      const int p = (int)threadIdx.x + i * NT;
+      if (p / (KCI * FV) < ns_k && p % (KCI * FV) < kin * FV) rb[p] = R[i];
     }
   };
   // Hand-off copy of chunk k's h history (LDS) to the global sequence buffer.
   auto copy_out = [&](int k) {
     const int nel = min(CH, Tt - k * CH) * (KCR * FV);
+    const f16x8* hb = hist + (k & 1) * kHistBuf;
     f16x8* dst = out_seq_h + (size_t)k * CH * hstep;
+    f16x8 v[RN];
+#pragma unroll
+    for (int i = 0; i < RN; ++i) v[i] = hb[min((int)threadIdx.x + i * NT, nel - 1)];
 #pragma unroll
     for (int i = 0; i < RN; ++i) {
       const int idx = threadIdx.x + i * NT;
-      if (idx < nel) dst[idx] = hist[idx];
+      if (idx < nel) {
+        // agent-scope relaxed stores (sc1): visible to other CUs and XCDs once complete, with no L2
+        // write-back at the publication
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(&v[i]);
+        uint64_t* d = reinterpret_cast<uint64_t*>(dst + idx);
+        __hip_atomic_store(d, src[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(d + 1, src[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   };
   auto need_for = [&](int k) -> uint32_t { return (uint32_t)min((k + 1) * CH, Tt); };  // chunk k published
 
-  int wait_idx = 0;
-  auto wait_up = [&](uint32_t need) -> bool {  // blocking wait for the upstream layer
-    const int slot = wait_idx++ & 1;
-    if (threadIdx.x == sync_tid) s_ok[slot] = wait_counter(up_ctr, need, a.status, a.wait_ticks);
-    __syncthreads();
-    return s_ok[slot] != 0;
-  };
-
   int probe_i = 0;
   // Probe steps are wave-uniform and kept in SGPRs (readfirstlane right after the load): a VGPR
   // loaded in the loop would make the compiler wait for every outstanding global access (vmcnt(0),
-  // in order on gfx950, so the chunk prefetch and the hand-off stores included) at each step.
+  // in order on gfx950, so the chunk loads and the hand-off stores included) at each step.
   int probe_next = a.n_probe > 0 ? __builtin_amdgcn_readfirstlane(a.probe_steps[0]) : -1;
   auto write_probe = [&](int p) {
     if (!row_ok) return;
@@ -203,35 +219,130 @@ lstm_wavefront_kernel(ForwardArgs a) {
     }
   };
 
-  for (int i = threadIdx.x; i < CH * KCI * FV; i += NT) ring[i] = f16x8{};
+  for (int i = threadIdx.x; i < 2 * kRingBuf; i += NT) ring[i] = f16x8{};
   __syncthreads();
 
   bool ok = true;
-  uint32_t poll = 0;  // deferred observation of the upstream counter (sync_tid only)
   if (Tt > 0) {
-    if (has_up) ok = wait_up(need_for(0));
+    if (has_up) {
+      if (threadIdx.x == sync_tid) s_ok = wait_counter(up_ctr, need_for(0), a.status, a.wait_ticks);
+      __syncthreads();
+      ok = s_ok != 0;
+    }
     if (ok) {
       load_chunk(0);
       store_chunk(0);
     }
-    if (ok && nchunk > 1) {
-      if (has_up) ok = wait_up(need_for(1));
-      if (ok) load_chunk(1);
-    }
-    if (has_up && threadIdx.x == sync_tid) poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();  // ring (chunk 0) and the initial h visible
+  __syncthreads();  // ring buffer 0 and the initial h visible
 
+  // Hand-off schedule, by step s of chunk k (each step ends with the LDS barrier):
+  //   s = 0       copy chunk k-1's h (history buffer (k-1) & 1) to the hand-off buffer with sc1
+  //               stores; the polling lane reads the upstream counter (for chunk k+1)
+  //   s = 1       every wave waits for its hand-off stores; the polling lane checks the counter
+  //               (bounded wait if chunk k+1 is not yet published, then an agent-scope acquire)
+  //               and shares the verdict through LDS
+  //   s = 2       publish chunk k-1 (relaxed counter store: the stores of every wave completed
+  //               before the barrier of step 1); load chunk k+1's inputs into VGPRs
+  //   s = CH - 2  write them into ring buffer (k+1) & 1, read from step CH - 1 on
+  // so layer l+1 runs two chunks and two steps behind layer l and no step waits on global memory.
   const bool hi = ibase != 0;
-  for (int k = 0; ok && k < nchunk; ++k) {
-    if (k > 0) {
-      // Chunk boundary: hand chunk k-1's h to global memory, move chunk k's input from VGPRs into
-      // the ring, acquire chunk k+1 of the upstream layer and start loading it.
-      __syncthreads();
-      if (has_down) copy_out(k - 1);
-      store_chunk(k);
-      const bool more = k + 1 < nchunk;
-      const int slot = wait_idx++ & 1;
+  uint32_t poll = 0;
+  f32x4 acc_next[4];
+  if (ok && Tt > 0) {
+    const f16x8* xr = ring + fl;
+    f16x8 xv[KCI];
+#pragma unroll
+    for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
+#pragma unroll
+    for (int kc = 0; kc < KCI; ++kc)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
+  }
+  // One step (t = k * CH + s).  Inlined with constant s for the steps of full chunks, so the
+  // hand-off schedule costs no branches on the other steps; returns false if a wait failed.
+  auto step = [&](const int t, const int s, const int k, const bool more) __attribute__((always_inline)) -> bool {
+    if (s == 0) {
+      if (has_down && k > 0) copy_out(k - 1);
+      if (has_up && more && threadIdx.x == sync_tid)
+        poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (s == 2) {
+      if (has_down && k > 0 && threadIdx.x == 0)
+        __hip_atomic_store(my_ctr, (uint32_t)(k * CH), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (more && has_up && s_ok == 0) return false;
+      load_chunk(more ? k + 1 : k);
+    }
+
+    f32x4 acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = acc_next[q];
+    // Recurrent part: h_{t-1} from the history slot of the previous step.
+    const f16x8* hr = hist + (((t + 2 * CH - 1) / CH) & 1) * kHistBuf + ((t + CH - 1) % CH) * (KCR * FV) + fl;
+    f16x8 hv[KCR];
+#pragma unroll
+    for (int kr = 0; kr < KCR; ++kr) hv[kr] = hr[kr * FV];
+#pragma unroll
+    for (int kr = 0; kr < KCR; ++kr)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[KCI + kr][q], hv[kr], acc[q], 0, 0, 0);
+
+    // Next step's input part (the last step recomputes a discarded in-range step), interleaved
+    // with this step's gate math: each (unit, row) piece of the epilogue is preceded by its share
+    // of the next step's MFMAs and fenced with sched_barrier, so the matrix core runs while the
+    // VALU evaluates the gates (in-order issue would otherwise queue all VALU work behind the
+    // MFMAs).
+    const int tn = min(t + 1, Tt - 1);
+    const f16x8* xr = ring + ((tn / CH) & 1) * kRingBuf + (tn % CH) * (KCI * FV) + fl;
+    f16x8 xv[KCI];
+#pragma unroll
+    for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
+    const bool live = t < len;
+    constexpr int kMfmaPerPiece = (KCI * 4 + UPL - 1) / UPL;
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+#pragma unroll
+      for (int m = j * kMfmaPerPiece; m < (j + 1) * kMfmaPerPiece && m < KCI * 4; ++m) {
+        const int kc = m / 4, q = m % 4;
+        acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
+      }
+      // this lane's pair j: D element ibase + j of every gate tile (one v_cndmask each)
+      float z[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) z[q] = pick(hi, acc[q][j], acc[q][2 + j % 2]);
+      float cn = c[j], hn;
+      lstm_cell(z[0], z[1], z[2], z[3], cn, hn);
+      if constexpr (RAGGED) {
+        // selects, not a branch: rows past their length keep their state
+        c[j] = live ? cn : c[j];
+        hcur[j] = live ? (_Float16)hn : hcur[j];
+      } else {
+        c[j] = cn;
+        hcur[j] = (_Float16)hn;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    *reinterpret_cast<hvec*>(hist_h(t)) = hcur;
+    if (!has_down && a.out_seq && row_ok) {
+      _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
+#pragma unroll
+      for (int j = 0; j < UPL; ++j)
+        if (uo + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
+    }
+    if (t + 1 == probe_next) {
+      write_probe(probe_i);
+      ++probe_i;
+      probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
+    }
+    if (s == 1) {
+      // Hand-off stores of step 0 complete before the barrier, so the counter published at step 2
+      // covers every wave's stores.
+      if (has_down && k > 0) __builtin_amdgcn_s_waitcnt(0);
       if (has_up && more && threadIdx.x == sync_tid) {
         const uint32_t need = need_for(k + 1);
         int okv;
@@ -241,104 +352,26 @@ lstm_wavefront_kernel(ForwardArgs a) {
         } else {
           okv = wait_counter(up_ctr, need, a.status, a.wait_ticks);
         }
-        poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_ok[slot] = okv;
+        s_ok = okv;
       }
-      __syncthreads();  // also orders every wave's hand-off stores before the publication below
-      if (has_up && more && s_ok[slot] == 0) {
+    } else if (s == CH - 2 && more) {
+      store_chunk(k + 1);
+    }
+    lds_barrier();
+    return true;
+  };
+  const int nfull = Tt / CH;
+  for (int k = 0; ok && k < nfull; ++k) {
+    const bool more = k + 1 < nchunk;
+#pragma unroll
+    for (int s = 0; s < CH; ++s)
+      if (!step(k * CH + s, s, k, more)) {
         ok = false;
         break;
       }
-      if (more) load_chunk(k + 1);
-    }
-
-    const int ns = min(CH, Tt - k * CH);
-    // Chunk k-1 is published halfway through chunk k: its stores have drained by then, so the
-    // release costs the publishing wave little.
-    const int pub_s = (k > 0 && has_down) ? min(CH / 2, ns - 1) : -1;
-    f32x4 acc_next[4];
-    {
-      const f16x8* xr = ring + fl;
-      f16x8 xv[KCI];
-#pragma unroll
-      for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
-#pragma unroll
-      for (int kc = 0; kc < KCI; ++kc)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
-    }
-    for (int s = 0; s < ns; ++s) {
-      const int t = k * CH + s;
-      f32x4 acc[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = acc_next[q];
-      // Recurrent part: h_{t-1} from the history slot of the previous step.
-      const f16x8* hr = hist + (s == 0 ? CH - 1 : s - 1) * (KCR * FV) + fl;
-      f16x8 hv[KCR];
-#pragma unroll
-      for (int kr = 0; kr < KCR; ++kr) hv[kr] = hr[kr * FV];
-#pragma unroll
-      for (int kr = 0; kr < KCR; ++kr)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[KCI + kr][q], hv[kr], acc[q], 0, 0, 0);
-
-      // Next step's input part (the chunk's last step recomputes a discarded in-range step),
-      // interleaved with this step's gate math: each (unit, row) piece of the epilogue is preceded
-      // by its share of the next step's MFMAs and fenced with sched_barrier, so the matrix core
-      // runs while the VALU evaluates the gates (in-order issue would otherwise queue all VALU
-      // work behind the MFMAs).
-      const f16x8* xr = ring + min(s + 1, ns - 1) * (KCI * FV) + fl;
-      f16x8 xv[KCI];
-#pragma unroll
-      for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
-      const bool live = t < len;
-      constexpr int kMfmaPerPiece = (KCI * 4 + UPL - 1) / UPL;
-#pragma unroll
-      for (int j = 0; j < UPL; ++j) {
-#pragma unroll
-        for (int m = j * kMfmaPerPiece; m < (j + 1) * kMfmaPerPiece && m < KCI * 4; ++m) {
-          const int kc = m / 4, q = m % 4;
-          acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
-        }
-        // this lane's pair j: D element ibase + j of every gate tile (one v_cndmask each)
-        float z[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) z[q] = pick(hi, acc[q][j], acc[q][2 + j % 2]);
-        float cn = c[j], hn;
-        lstm_cell(z[0], z[1], z[2], z[3], cn, hn);
-        if constexpr (RAGGED) {
-          // selects, not a branch: rows past their length keep their state
-          c[j] = live ? cn : c[j];
-          hcur[j] = live ? (_Float16)hn : hcur[j];
-        } else {
-          c[j] = cn;
-          hcur[j] = (_Float16)hn;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      *reinterpret_cast<hvec*>(hist_h(s)) = hcur;
-      if (!has_down && a.out_seq && row_ok) {
-        _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + uo;
-#pragma unroll
-        for (int j = 0; j < UPL; ++j)
-          if (uo + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
-      }
-      if (t + 1 == probe_next) {
-        write_probe(probe_i);
-        ++probe_i;
-        probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
-      }
-      if (s == pub_s && threadIdx.x == 0)
-        __hip_atomic_store(my_ctr, (uint32_t)(k * CH), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-      lds_barrier();
-    }
   }
+  for (int t = nfull * CH; ok && t < Tt; ++t)
+    if (!step(t, t - nfull * CH, nfull, false)) ok = false;
 
   if (!ok) {
     // A hand-off wait failed (the status word records it and fails every other wait): poison this
@@ -352,10 +385,10 @@ lstm_wavefront_kernel(ForwardArgs a) {
     return;
   }
   if (has_down && Tt > 0) {
-    __syncthreads();
     copy_out(nchunk - 1);
+    __builtin_amdgcn_s_waitcnt(0);  // every wave's hand-off stores complete before the counter moves
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(my_ctr, (uint32_t)Tt, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(my_ctr, (uint32_t)Tt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // Steps past the tile's longest row were never visited: their output sequence is zero.
@@ -387,7 +420,8 @@ lstm_wavefront_kernel(ForwardArgs a) {
 
   // Linear head on the final h of the last layer (history slot of the tile's last step).
   if (!has_down && a.out) {
-    const _Float16* hf = reinterpret_cast<const _Float16*>(hist + ((Tt + CH - 1) % CH) * (KCR * FV));
+    const _Float16* hf = reinterpret_cast<const _Float16*>(hist + (((Tt - 1 + 2 * CH) / CH) & 1) * kHistBuf +
+                                                           ((Tt - 1 + 2 * CH) % CH) * (KCR * FV));
     for (int idx = threadIdx.x; idx < ROWS * a.O; idx += NT) {
       const int rr = idx / a.O, o = idx % a.O;
       const int g = a.row0 + tile * ROWS + rr;

@@ -178,25 +178,21 @@ lstm_wavefront_kernel(ForwardArgs a) {
       if (p / (KCI * FV) < ns_k && p % (KCI * FV) < kin * FV) rb[p] = R[i];
     }
   };
-  // Hand-off copy of chunk k's h history (LDS) to the global sequence buffer.
+  // Hand-off copy of chunk k's h history (LDS) to the global sequence buffer, in 8-byte words so
+  // that each wave's agent-scope (sc1) store covers one contiguous 512-byte run: sc1 stores are
+  // written through, and two interleaved 8-byte halves of 16-byte elements would each cost a full
+  // line write.  They become visible to other CUs and XCDs once complete, with no L2 write-back.
   auto copy_out = [&](int k) {
-    const int nel = min(CH, Tt - k * CH) * (KCR * FV);
-    const f16x8* hb = hist + (k & 1) * kHistBuf;
-    f16x8* dst = out_seq_h + (size_t)k * CH * hstep;
-    f16x8 v[RN];
+    const int nw = min(CH, Tt - k * CH) * (KCR * FV) * 2;
+    const uint64_t* hb = reinterpret_cast<const uint64_t*>(hist + (k & 1) * kHistBuf);
+    uint64_t* dst = reinterpret_cast<uint64_t*>(out_seq_h + (size_t)k * CH * hstep);
+    uint64_t v[2 * RN];
 #pragma unroll
-    for (int i = 0; i < RN; ++i) v[i] = hb[min((int)threadIdx.x + i * NT, nel - 1)];
+    for (int i = 0; i < 2 * RN; ++i) v[i] = hb[min((int)threadIdx.x + i * NT, nw - 1)];
 #pragma unroll
-    for (int i = 0; i < RN; ++i) {
+    for (int i = 0; i < 2 * RN; ++i) {
       const int idx = threadIdx.x + i * NT;
-      if (idx < nel) {
-        // agent-scope relaxed stores (sc1): visible to other CUs and XCDs once complete, with no L2
-        // write-back at the publication
-        const uint64_t* src = reinterpret_cast<const uint64_t*>(&v[i]);
-        uint64_t* d = reinterpret_cast<uint64_t*>(dst + idx);
-        __hip_atomic_store(d, src[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(d + 1, src[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      if (idx < nw) __hip_atomic_store(dst + idx, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
   auto need_for = [&](int k) -> uint32_t { return (uint32_t)min((k + 1) * CH, Tt); };  // chunk k published

@@ -229,13 +229,20 @@ class NativeLibrary:
         c_n = torch.empty((L, B, H), **opts) if want_state else None
         lens_dev = None
         if lengths is not None:
+            # Host lengths (a list or CPU tensor, as torch.nn.utils.rnn.pack_padded_sequence takes
+            # them) are checked on the host and reach the device through pinned memory without a
+            # stream synchronisation; device-resident lengths are copied back for the check, which
+            # synchronises the stream.
             lens = torch.as_tensor(lengths)
             if lens.dim() != 1 or int(lens.numel()) != B:
                 raise ValueError("lengths must be a 1-D tensor with one entry per batch row")
             lc = lens.detach().to("cpu", torch.int64)
             if B and (int(lc.min()) < 0 or int(lc.max()) > T):
                 raise ValueError(f"lengths must lie in [0, {T}]")
-            lens_dev = lens.to(device=device, dtype=torch.int32).contiguous()
+            if lens.device.type == "cpu":
+                lens_dev = lc.to(torch.int32).contiguous().pin_memory().to(device, non_blocking=True)
+            else:
+                lens_dev = lens.to(device=device, dtype=torch.int32).contiguous()
         states = []
         for s in (h0, c0):
             if s is None:

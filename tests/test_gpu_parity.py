@@ -119,6 +119,34 @@ def test_ragged_small_unsorted_with_zero_length(gpu):
     np.testing.assert_allclose(got[3], native.linear.bias.detach().numpy(), atol=2e-3)
 
 
+def test_ragged_length_sources_and_back_to_back_calls(gpu):
+    """Lengths as a list, a strided host tensor and a device tensor give the same result, and
+    back-to-back calls with different host lengths (staged through pinned memory without a stream
+    synchronisation) each see their own lengths."""
+    I, H, L, O, B, T = 5, 128, 3, 6, 40, 48
+    _say("ragged length sources")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    xd = x.to("cuda", torch.float16)
+    model = _gpu_model(native)
+    g = torch.Generator().manual_seed(11)
+    wide = torch.randint(0, T + 1, (2 * B,), generator=g)
+    base = wide[::2]  # strided host tensor
+    assert not base.is_contiguous()
+    want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
+                                    lengths=base.numpy())
+    for src in (base.tolist(), base, base.to("cuda")):
+        got = model.forward_ragged(xd, src).float().cpu().numpy()
+        assert_close(got, want, what=f"lengths from {type(src).__name__}")
+    sets = [torch.randint(1, T + 1, (B,), generator=g) for _ in range(4)]
+    outs = [model.forward_ragged(xd, s) for s in sets]  # no synchronisation between the calls
+    for s, o in zip(sets, outs):
+        ref = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
+                                       lengths=s.numpy())
+        assert_close(o.float().cpu().numpy(), ref, what="back-to-back ragged call")
+    gpu.check_status(torch.device("cuda"))
+
+
 def test_persistent_lstm_dropin(gpu):
     I, H, L, B, T = 5, 128, 2, 24, 50
     _say("PersistentLSTM drop-in")

@@ -139,6 +139,10 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
   }
+  // Wait for the resident weights here: otherwise the compiler keeps them "possibly outstanding"
+  // into the step loop and puts vmcnt waits before the input waves' MFMAs, which (one in-order
+  // counter on gfx950) then wait for the gather loads those MFMAs are meant to overlap.
+  __builtin_amdgcn_s_waitcnt(0);
   for (int idx = threadIdx.x; idx < 4 * HS / 2; idx += NT) {
     const int q = idx / (HS / 2), up = idx % (HS / 2);
     const float* b = a.bias + ((size_t)layer * 4 + q) * HP + slice * HS + 2 * up;
@@ -414,6 +418,12 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   __syncthreads();
 
   uint32_t unpublished = 0;  // steps computed since the last publication
+  // Two-tile workgroups: the upstream polls before the loop load into VGPRs that the compiler
+  // otherwise treats as possibly outstanding at the loop head, which put a vmcnt(0) (waiting for
+  // the other tile's gather) in front of every tile-step's MFMAs.  One wait here costs the first
+  // chunk's prefetch once (measured: C3 6.2 -> 5.7 ms; with one tile it is 2% slower, so only
+  // two-tile workgroups take it).
+  if constexpr (NTI == 2) __builtin_amdgcn_s_waitcnt(0);
   for (int k = 0; ok && k < nchunk; ++k) {
     if (k > 0) {
       if (has_down && k % PUB == 0) {

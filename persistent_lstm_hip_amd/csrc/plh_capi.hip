@@ -226,9 +226,10 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   uint32_t* status = (uint32_t*)(ws + w.status);
   uint32_t* counters = (uint32_t*)(ws + w.counters);
 
-  err = plh::launch_zero_u32(status, 1, s);
-  if (err != hipSuccess) return fail_hip(err, "status reset");
-  if (batch == 0) return PLH_OK;
+  if (batch == 0) {
+    err = plh::launch_zero_u32(status, 1, s);
+    return err == hipSuccess ? PLH_OK : fail_hip(err, "status reset");
+  }
 
   plh::ForwardArgs a;
   std::memset(&a, 0, sizeof(a));
@@ -259,7 +260,7 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   a.H = g.H;
   a.L = g.L;
   a.O = g.O;
-  a.kc_in0 = g.kc_in0;
+  a.g_in0 = g.g_in0;
   a.wait_ticks = (uint64_t)g_wait_us * 100u;  // s_memrealtime: 100 MHz
 
   const bool timed = g_timing.used * 2 < (int)g_timing.ev.size();
@@ -273,14 +274,10 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     a.ntile = (a.ntile + a.wg_tiles - 1) / a.wg_tiles * a.wg_tiles;
     a.rows_pad = a.ntile * plan.tile_rows;
     a.xcd_map = (g.slices > 1 ? (g.L * a.ntile / a.wg_tiles) % 8 : a.ntile % 8) == 0 ? 1 : 0;
-    err = plh::launch_zero_u32(counters, (size_t)g.L * a.ntile, s);
-    if (err != hipSuccess) return fail_hip(err, "counter reset");
-    if (g.slices > 1) {  // tags restart at 1: clear the exchange ring of this launch's tiles
-      err = plh::launch_zero_u32((uint32_t*)a.xring, (size_t)g.L * a.ntile * 2 * g.HP * 8 * 2, s);
-      if (err != hipSuccess) return fail_hip(err, "exchange ring reset");
-    }
-    err = plh::launch_pack_x(g, a, s);
-    if (err != hipSuccess) return fail_hip(err, "x packing");
+    // x of this launch's rows into xp; status (first launch), counters and, when sliced, the
+    // exchange ring (tags restart at 1) cleared: one launch ahead of the persistent one
+    err = plh::launch_forward_prologue(g, a, row0 == 0 ? status : nullptr, s);
+    if (err != hipSuccess) return fail_hip(err, "forward prologue");
     if (timed && row0 == 0) {
       err = hipEventRecord(g_timing.ev[2 * g_timing.used], s);
       if (err != hipSuccess) return fail_hip(err, "timing event");

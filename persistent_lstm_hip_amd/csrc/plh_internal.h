@@ -23,7 +23,7 @@ struct Geometry {
   int waves;   // waves per workgroup: HP / 16 (one per 16 hidden units) or 8 when sliced
   int kci;     // input-part K chunks of 32 for layers >= 1 (= HP / 32)
   int kc;      // K chunks of [W_ih | W_hh] per gate row (= 2 * kci)
-  int kc_in0;  // input-part K chunks layer 0 uses (= ceil(I / 32) <= kci)
+  int g_in0;   // 8-wide K groups of x per step that layer 0 reads (= ceil(I / 8) <= 4 * kci)
 };
 
 // Fills *g; returns false (with the reason) for geometries the kernels do not implement.
@@ -43,7 +43,9 @@ PackedLayout packed_layout(const Geometry& g);
 // Workspace of one persistent launch (reused by successive batch chunks); R = rows per tile:
 //   status   u32                                   PLH_STATUS_* bits
 //   counters u32 [L][ntile]                        steps published per (layer, tile)
-//   xp       f16x8 [ntile][T][kc_in0][4][R]        x in B-fragment order (layer 0 input)
+//   xp       f16x8 [ntile][T][g_in0][R]            x in B-fragment order (layer 0 input): group g
+//                                                  holds k = 8g .. 8g+7, the first g_in0 * R
+//                                                  entries of a step's fragment blocks
 //   hseq     f16x8 [L-1][ntile][T][kci][4][R]      h of layers 0..L-2 in B-fragment order
 //   xring    u64 [L][ntile][2][HP * 8]             sliced geometries only: per-step exchange of h
 //                                                  among the slices of a (layer, tile), tagged words
@@ -81,7 +83,7 @@ struct ForwardArgs {
   int row0, row_end;            // batch rows [row0, row_end) handled by this launch
   int rows_pad, ntile;          // rows_pad = tile_rows * ntile
   int tile_rows;                // batch rows per workgroup: 8 or 16
-  int kc_in0;
+  int g_in0;                    // 8-wide K groups of x per step in xp
   int xcd_map;                  // 1: keep a tile's layer chain on one XCD
   uint64_t wait_ticks;          // bound on one inter-workgroup wait, in s_memrealtime ticks (100 MHz)
   int wg_tiles;                 // sliced kernels: 16-row tiles per workgroup (1 or 2); ntile is a multiple
@@ -93,7 +95,9 @@ hipError_t launch_pack_bias(const Geometry& g, int layer, const _Float16* b_ih, 
                             float* bias, hipStream_t s);
 hipError_t launch_pack_linear(const Geometry& g, const _Float16* w, const _Float16* b, float* wlin,
                               float* blin, hipStream_t s);
-hipError_t launch_pack_x(const Geometry& g, const ForwardArgs& a, hipStream_t s);
+// One launch before each persistent launch: packs this launch's x into xp and clears the status
+// word (if `status`), the counters and (sliced) the exchange ring.
+hipError_t launch_forward_prologue(const Geometry& g, const ForwardArgs& a, uint32_t* status, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t s);
 hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, int cols, hipStream_t s);
 

@@ -37,7 +37,7 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
   g->waves = g->slices > 1 ? 8 : HP / 16;
   g->kci = HP / 32;
   g->kc = 2 * g->kci;
-  g->kc_in0 = (I + 31) / 32;
+  g->g_in0 = (I + 7) / 8;
   return true;
 }
 
@@ -69,7 +69,7 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   w.status = 0;
   w.counters = 256;
   w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile);
-  w.hseq = align256(w.xp + ntile * seq_len * g.kc_in0 * frag_bytes);
+  w.hseq = align256(w.xp + ntile * seq_len * g.g_in0 * tile_rows * 16);
   w.xring = align256(w.hseq + (size_t)(g.L - 1) * ntile * seq_len * g.kci * frag_bytes);
   w.xring_words = g.slices > 1 ? (size_t)g.L * ntile * 2 * g.HP * 8 : 0;
   w.total = align256(w.xring + w.xring_words * sizeof(uint64_t));

@@ -1,5 +1,7 @@
 // plh_pack.hip -- the layout kernels of the forward: weight packing into per-lane MFMA fragments,
 // x into B-fragment order, and small fills.
+#include <algorithm>
+
 #include "plh_device.h"
 
 namespace plh {
@@ -96,19 +98,25 @@ __global__ void pack_linear_kernel(const _Float16* __restrict__ w, const _Float1
 
 // x [B, T, I] -> xp [ntile][T][kci0][4][rows] f16x8: B-fragment order for tiles of `rows` rows,
 // zero padded.
-__global__ void pack_x_kernel(const _Float16* __restrict__ x, int T, int I, int row0, int row_end, int ntile,
-                              int rows, int kci0, f16x8* __restrict__ xp) {
+// Forward prologue: x of rows [row0, row_end) into xp (B-fragment order: per tile and step, g0
+// 8-wide K groups of `rows` f16x8, zero past I and past row_end), and the zeroing of up to three
+// u32 ranges (status, counters, exchange ring), in one launch.
+__global__ void forward_prologue_kernel(const _Float16* __restrict__ x, int T, int I, int row0, int row_end,
+                                        int ntile, int rows, int g0, f16x8* __restrict__ xp,
+                                        uint32_t* __restrict__ z0, size_t n0, uint32_t* __restrict__ z1,
+                                        size_t n1, uint32_t* __restrict__ z2, size_t n2) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int fv = 4 * rows;
-  const size_t total = (size_t)ntile * T * kci0 * fv;
-  if (e >= total) return;
-  const int f = (int)(e % fv);
-  const int kc = (int)((e / fv) % kci0);
-  const size_t tt = e / ((size_t)fv * kci0);
+  if (e < n0) z0[e] = 0u;
+  if (e < n1) z1[e] = 0u;
+  if (e < n2) z2[e] = 0u;
+  const int per = g0 * rows;
+  if (e >= (size_t)ntile * T * per) return;
+  const int f = (int)(e % per);
+  const size_t tt = e / per;
   const int t = (int)(tt % T);
   const int tile = (int)(tt / T);
   const int b = row0 + tile * rows + f % rows;
-  const int k0 = kc * 32 + (f / rows) * 8;
+  const int k0 = (f / rows) * 8;
   f16x8 v = {};
   if (b < row_end) {
     const _Float16* src = x + ((size_t)b * T + t) * I;
@@ -165,11 +173,16 @@ hipError_t launch_pack_linear(const Geometry& g, const _Float16* w, const _Float
   return hipGetLastError();
 }
 
-hipError_t launch_pack_x(const Geometry& g, const ForwardArgs& a, hipStream_t s) {
-  const size_t n = (size_t)a.ntile * a.T * g.kc_in0 * 4 * a.tile_rows;
+hipError_t launch_forward_prologue(const Geometry& g, const ForwardArgs& a, uint32_t* status, hipStream_t s) {
+  const size_t npack = (size_t)a.ntile * a.T * g.g_in0 * a.tile_rows;
+  const size_t nstat = status ? 1 : 0;
+  const size_t nctr = (size_t)g.L * a.ntile;
+  const size_t nring = g.slices > 1 ? (size_t)g.L * a.ntile * 2 * g.HP * 8 * 2 : 0;  // u64 words as u32
+  const size_t n = std::max(std::max(npack, nstat), std::max(nctr, nring));
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(pack_x_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, a.I, a.row0, a.row_end, a.ntile,
-                     a.tile_rows, g.kc_in0, a.xp);
+  hipLaunchKernelGGL(forward_prologue_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, a.I, a.row0, a.row_end,
+                     a.ntile, a.tile_rows, g.g_in0, a.xp, status, nstat, a.counters, nctr,
+                     reinterpret_cast<uint32_t*>(a.xring), nring);
   return hipGetLastError();
 }
 

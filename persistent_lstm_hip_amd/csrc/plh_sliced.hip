@@ -177,12 +177,12 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 
   const bool has_up = layer > 0;
   const bool has_down = layer + 1 < a.L;
-  const int kin = has_up ? KCH : a.kc_in0;
+  const int per = has_up ? KCH * FV : a.g_in0 * 16;  // input f16x8 per step in the source
   const size_t hstep = (size_t)KCH * FV;
   const int tile0 = tgrp * NTI;  // first 16-row tile of this workgroup
   auto in_seq = [&](int i) -> const f16x8* {
     return has_up ? a.hseq + ((size_t)(layer - 1) * a.ntile + tile0 + i) * a.T * hstep
-                  : a.xp + (size_t)(tile0 + i) * a.T * kin * FV;
+                  : a.xp + (size_t)(tile0 + i) * a.T * per;
   };
   auto my_seq = [&](int i) -> f16x8* { return a.hseq + ((size_t)layer * a.ntile + tile0 + i) * a.T * hstep; };
   auto xr = [&](int i) -> uint64_t* { return a.xring + ((size_t)layer * a.ntile + tile0 + i) * 2 * C::kWords; };
@@ -207,12 +207,14 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 
   const int nchunk = (Tt + CH - 1) / CH;
   f16x8 R[NTI][RN];
+  // A step's source holds the first `per` of its KCH * FV ring entries (layer 0: the g_in0 8-wide K
+  // groups of x; the rest of the ring stays zero from the initialisation).
   auto load_chunk = [&](int k) {
     const int s0 = k * CH;
-    const int nel = min(CH, Tt - s0) * kin * FV;
+    const int nel = min(CH, Tt - s0) * per;
 #pragma unroll
     for (int i = 0; i < NTI; ++i) {
-      const f16x8* src = in_seq(i) + (size_t)s0 * kin * FV;
+      const f16x8* src = in_seq(i) + (size_t)s0 * per;
 #pragma unroll
       for (int r = 0; r < RN; ++r) {
         const int idx = threadIdx.x + r * NT;
@@ -221,7 +223,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     }
   };
   auto store_chunk = [&](int k) {
-    const int per = kin * FV;
     const int nel = min(CH, Tt - k * CH) * per;
 #pragma unroll
     for (int i = 0; i < NTI; ++i)

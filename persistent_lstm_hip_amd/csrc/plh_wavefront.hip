@@ -144,10 +144,10 @@ lstm_wavefront_kernel(ForwardArgs a) {
 
   const bool has_up = layer > 0;
   const bool has_down = layer < a.L - 1;
-  const int kin = has_up ? KCI : a.kc_in0;  // input fragment blocks per step
+  const int per = has_up ? KCI * FV : a.g_in0 * ROWS;  // input f16x8 per step in the source
   const size_t hstep = (size_t)KCR * FV;     // f16x8 per (tile, step) in the hand-off buffer
   const f16x8* in_seq = has_up ? a.hseq + ((size_t)(layer - 1) * a.ntile + tile) * a.T * hstep
-                               : a.xp + (size_t)tile * a.T * kin * FV;
+                               : a.xp + (size_t)tile * a.T * per;
   f16x8* out_seq_h = has_down ? a.hseq + ((size_t)layer * a.ntile + tile) * a.T * hstep : nullptr;
   const uint32_t* up_ctr = has_up ? a.counters + (layer - 1) * a.ntile + tile : nullptr;
   uint32_t* my_ctr = a.counters + layer * a.ntile + tile;
@@ -155,18 +155,19 @@ lstm_wavefront_kernel(ForwardArgs a) {
 
   const int nchunk = (Tt + CH - 1) / CH;
   // Chunk k's step inputs: loaded into VGPRs (R) 4 steps before they are needed, written to ring
-  // buffer k & 1 at step CH - 2.  Every lane loads (indices clamped into the chunk), so the loads
-  // write R directly; positions that hold no data are not written (layer 0 fills the first kin
-  // fragment blocks of a step, the rest stay zero from the initialisation).
+  // buffer k & 1 at step CH - 2.  Thread positions are ring positions; a step's source holds the
+  // first `per` of its KCI * FV ring entries (layer 0: the g_in0 8-wide K groups of x, the rest stay
+  // zero from the initialisation).  Every lane loads (indices clamped into the chunk), so the loads
+  // write R directly.
   f16x8 R[RN];
   auto load_chunk = [&](int k) {
     const int ns_k = min(CH, Tt - k * CH);
-    const f16x8* src = in_seq + (size_t)k * CH * kin * FV;
+    const f16x8* src = in_seq + (size_t)k * CH * per;
 #pragma unroll
     for (int i = 0; i < RN; ++i) {
       const int p = (int)threadIdx.x + i * NT;
-      const int st = min(p / (KCI * FV), ns_k - 1), e = min(p % (KCI * FV), kin * FV - 1);
-      R[i] = src[st * kin * FV + e];
+      const int st = min(p / (KCI * FV), ns_k - 1), e = min(p % (KCI * FV), per - 1);
+      R[i] = src[st * per + e];
     }
   };
   auto store_chunk = [&](int k) {
@@ -175,7 +176,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
 #pragma unroll
     for (int i = 0; i < RN; ++i) {
       const int p = (int)threadIdx.x + i * NT;
-      if (p / (KCI * FV) < ns_k && p % (KCI * FV) < kin * FV) rb[p] = R[i];
+      if (p / (KCI * FV) < ns_k && p % (KCI * FV) < per) rb[p] = R[i];
     }
   };
   // Hand-off copy of chunk k's h history (LDS) to the global sequence buffer, in 8-byte words so

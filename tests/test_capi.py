@@ -95,7 +95,7 @@ def test_sliced_workspace_layout(ext):
         b = ext.workspace_bytes(5, H, L, 24, 512, T)
         handoff = (L - 1) * rows * T * H * 2
         ring = L * tiles * 2 * H * 8 * 8
-        xp = rows * T * 32 * 2  # x of the launch, padded to one 32-wide K chunk
+        xp = rows * T * 8 * 2  # x of the launch: one 8-wide K group (I = 5) per row and step
         assert handoff + ring + xp <= b < handoff + ring + xp + (1 << 12)
 
 

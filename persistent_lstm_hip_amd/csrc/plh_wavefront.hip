@@ -10,7 +10,8 @@
 //     the B columns 8..15 repeat rows 0..7 and each lane evaluates two of its four (unit, row)
 //     pairs; the next step's input part is issued between this step's gate computations;
 //   * the gate nonlinearities and the c/h update run on the accumulator registers; c never leaves
-//     VGPRs; h goes to an LDS history ring that also feeds the next step's recurrent MFMAs;
+//     VGPRs; h goes to an LDS history (double-buffered by chunk) that also feeds the next step's
+//     recurrent MFMAs and the hand-off copy;
 //   * activations live in "fragment order": a [R rows x 32 k] block is stored as [k/8][row][8],
 //     i.e. exactly the B operand of one MFMA (lane l reads 16 B at l * 16), in LDS and in the
 //     global hand-off buffer, so LDS traffic is conflict-free and global traffic contiguous;

@@ -42,6 +42,10 @@ __device__ __forceinline__ void lstm_cell(float zi, float zf, float zg, float zo
   c = cn;
 }
 
+// s_waitcnt on the vector-memory counter alone (vmcnt = 0; expcnt and lgkmcnt at their no-wait
+// maxima in the gfx9 encoding).  gfx950 retires loads and stores on this counter in issue order.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Barrier that orders LDS traffic only: global stores stay in flight across it.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");

@@ -229,6 +229,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
     }
     if (ok) {
       load_chunk(0);
+      wait_vmem_all();
       store_chunk(0);
     }
   }
@@ -268,6 +269,11 @@ lstm_wavefront_kernel(ForwardArgs a) {
       if (has_up && more && threadIdx.x == sync_tid)
         poll = __hip_atomic_load(up_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if (s == 2) {
+      // Nothing the step needs is outstanding here.  Without this explicit wait the compiler
+      // keeps the chunk loads "possibly outstanding" (their consumers, the ring writes, are
+      // lane-conditional) and waits for every access in flight -- the counter store below
+      // included -- before the recurrent LDS reads that reuse those registers.
+      wait_vmem_all();
       if (has_down && k > 0 && threadIdx.x == 0)
         __hip_atomic_store(my_ctr, (uint32_t)(k * CH), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (more && has_up && s_ok == 0) return false;
@@ -289,10 +295,8 @@ lstm_wavefront_kernel(ForwardArgs a) {
         acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[KCI + kr][q], hv[kr], acc[q], 0, 0, 0);
 
     // Next step's input part (the last step recomputes a discarded in-range step), interleaved
-    // with this step's gate math: each (unit, row) piece of the epilogue is preceded by its share
-    // of the next step's MFMAs and fenced with sched_barrier, so the matrix core runs while the
-    // VALU evaluates the gates (in-order issue would otherwise queue all VALU work behind the
-    // MFMAs).
+    // with this step's gate math so the matrix core runs while the VALU evaluates the gates
+    // (in-order issue would otherwise queue all VALU work behind a burst of MFMAs).
     const int tn = min(t + 1, Tt - 1);
     const f16x8* xr = ring + ((tn / CH) & 1) * kRingBuf + (tn % CH) * (KCI * FV) + fl;
     f16x8 xv[KCI];
@@ -301,15 +305,12 @@ lstm_wavefront_kernel(ForwardArgs a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
     const bool live = t < len;
-    constexpr int kMfmaPerPiece = (KCI * 4 + UPL - 1) / UPL;
-#pragma unroll
-    for (int j = 0; j < UPL; ++j) {
-#pragma unroll
-      for (int m = j * kMfmaPerPiece; m < (j + 1) * kMfmaPerPiece && m < KCI * 4; ++m) {
-        const int kc = m / 4, q = m % 4;
-        acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
-      }
-      // this lane's pair j: D element ibase + j of every gate tile (one v_cndmask each)
+    auto input_mfma = [&](int m) __attribute__((always_inline)) {
+      const int kc = m / 4, q = m % 4;
+      acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
+    };
+    // this lane's pair j: D element ibase + j of every gate tile (one v_cndmask each)
+    auto cell_pair = [&](int j) __attribute__((always_inline)) {
       float z[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) z[q] = pick(hi, acc[q][j], acc[q][2 + j % 2]);
@@ -323,7 +324,32 @@ lstm_wavefront_kernel(ForwardArgs a) {
         c[j] = cn;
         hcur[j] = (_Float16)hn;
       }
+    };
+    if constexpr (ROWS == 8) {
+      // Two pairs per lane (~80 VALU instructions per wave): one MFMA, then three VALU
+      // instructions, and so on, so both waves of a SIMD keep the matrix core fed and neither
+      // queues its gate math behind a burst of MFMAs.
       __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < KCI * 4; ++m) input_mfma(m);
+#pragma unroll
+      for (int j = 0; j < UPL; ++j) cell_pair(j);
+#pragma unroll
+      for (int m = 0; m < KCI * 4; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      // Four pairs per lane: each pair is preceded by its share of the MFMAs and fenced.
+      constexpr int kMfmaPerPiece = (KCI * 4 + UPL - 1) / UPL;
+#pragma unroll
+      for (int j = 0; j < UPL; ++j) {
+#pragma unroll
+        for (int m = j * kMfmaPerPiece; m < (j + 1) * kMfmaPerPiece && m < KCI * 4; ++m) input_mfma(m);
+        cell_pair(j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     *reinterpret_cast<hvec*>(hist_h(t)) = hcur;
     if (!has_down && a.out_seq && row_ok) {
@@ -352,8 +378,9 @@ lstm_wavefront_kernel(ForwardArgs a) {
         }
         s_ok = okv;
       }
-    } else if (s == CH - 2 && more) {
-      store_chunk(k + 1);
+    } else if (s == CH - 2) {
+      wait_vmem_all();  // chunk k+1's inputs, on every path (the ring writes are lane-conditional)
+      if (more) store_chunk(k + 1);
     }
     lds_barrier();
     return true;

@@ -284,19 +284,33 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     for (int q = 0; q < 4; ++q) part[pslot(i, t)][wave][q][lane] = acc[q];
   };
 
+  // Ring accesses.  Two-tile workgroups run out of VGPRs with global atomics, which hold a 64-bit
+  // VGPR address per word; they use buffer loads and stores instead: a descriptor of one ring slot
+  // (uniform, in SGPRs), the thread's byte offset in a VGPR and the word's block offset as the
+  // scalar offset, with cache policy sc1 (agent-scope coherent, as agent-scope relaxed atomics).
+  // Every offset stays inside the slot.  One-tile workgroups keep the global atomics: the extra
+  // SGPR pressure of the descriptors costs them more than the VGPRs save.
+  auto ring_rs = [&](int i, int t) {
+    return __builtin_amdgcn_make_buffer_rsrc(xr(i) + (size_t)(t & 1) * C::kWords, 0, C::kWords * 8, 0x00020000);
+  };
+  auto gload = [&](int i, int t, int r) -> uint64_t {
+    if constexpr (NTI == 2) {
+      return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(ring_rs(i, t), threadIdx.x * 8u, r * NT * 8, 16));
+    } else {
+      return load_agent_u64(xr(i) + (size_t)(t & 1) * C::kWords + threadIdx.x + r * NT);
+    }
+  };
   // Gather words of tile i, step t: issued right after the tile's own words are stored.
   uint64_t wv[NTI][NW];
   auto issue_gather = [&](int i, int t) {
-    const uint64_t* src = xr(i) + (size_t)(t & 1) * C::kWords + threadIdx.x;
 #pragma unroll
-    for (int r = 0; r < NW; ++r) wv[i][r] = load_agent_u64(src + r * NT);
+    for (int r = 0; r < NW; ++r) wv[i][r] = gload(i, t, r);
   };
   // Complete the gather of tile i, step t, into hbuf[i]: re-poll the words whose tag is not t + 1
   // yet.  Before spinning, the input waves compute tile i's partials for step t + 1 (ring slot
   // s_next; -1: none).  False (uniformly) if any wait of the workgroup failed.
   auto complete_gather = [&](int i, int t, int s_next) -> bool {
     if (!recurrent && s_next >= 0) partials(i, t + 1, s_next);
-    const uint64_t* src = xr(i) + (size_t)(t & 1) * C::kWords + threadIdx.x;
     const uint32_t want = (uint32_t)t + 1u;
     uint64_t t0 = 0;
     for (int spin = 0;; ++spin) {
@@ -317,9 +331,10 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
           break;
         }
       }
+      if constexpr (NTI == 2) asm volatile("" ::: "memory");  // the buffer loads re-read the ring every spin
 #pragma unroll
       for (int r = 0; r < NW; ++r)
-        if (word_tag(wv[i][r]) != want) wv[i][r] = load_agent_u64(src + r * NT);
+        if (word_tag(wv[i][r]) != want) wv[i][r] = gload(i, t, r);
     }
     uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf[i]);
 #pragma unroll
@@ -357,14 +372,25 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   auto store_h = [&](int i, int t) {
     if (!active) return;
     const bool live = t < len[i];
-    __hip_atomic_store(xr(i) + (size_t)(t & 1) * C::kWords + woff, tag_word(hcur[i][0], hcur[i][1], (uint32_t)t + 1u),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t word = tag_word(hcur[i][0], hcur[i][1], (uint32_t)t + 1u);
+    if constexpr (NTI == 2) {
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, word),
+                                            ring_rs(i, t), (uint32_t)woff * 8u, 0, 16);
+    } else {
+      __hip_atomic_store(xr(i) + (size_t)(t & 1) * C::kWords + woff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (has_down) {
       union { _Float16 h[2]; uint32_t u; } v;
       v.h[0] = hcur[i][0];
       v.h[1] = hcur[i][1];
-      __hip_atomic_store(reinterpret_cast<uint32_t*>(reinterpret_cast<_Float16*>(my_seq(i) + (size_t)t * hstep) + hoff),
-                         v.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (NTI == 2) {
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(my_seq(i) + (size_t)t * hstep, 0, (int)(hstep * 16), 0x00020000);
+        __builtin_amdgcn_raw_buffer_store_b32(v.u, rs, (uint32_t)hoff * 2u, 0, 16);
+      } else {
+        __hip_atomic_store(reinterpret_cast<uint32_t*>(reinterpret_cast<_Float16*>(my_seq(i) + (size_t)t * hstep) + hoff),
+                           v.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     if (!has_down && a.out_seq && row_ok[i]) {
       _Float16* dst = a.out_seq + ((size_t)grow[i] * a.T + t) * a.H + eu;

@@ -228,6 +228,9 @@ def main() -> int:
         kernel_ms_total, n_timed = ext.kernel_timing_read()
         ext.kernel_timing(0)
         ext.check_status(dev)
+    # On-box check of the roofline constant (after the timed region): the dense fp16 MFMA rate this
+    # GPU sustains with the kernels' instruction, and the shader clock meanwhile.
+    probe_tflops, probe_ghz = ext.probe_mfma_f16()
     uniform = uniform_batch_protocol(model, dev, args.warmup, args.steps)
     others = other_configs(dev) if not args.no_other_configs else None
     total_ms = t_all0.elapsed_time(t_all1)
@@ -275,6 +278,12 @@ def main() -> int:
             "frac": achieved / PEAK_FP16_TFLOPS,
             "traffic": read_traffic(),
             "flops_per_launch": flops,
+            "peak_probe": {
+                "tflops": probe_tflops,
+                "shader_clock_ghz": probe_ghz,
+                "what": "v_mfma_f32_16x16x32_f16, 8 independent accumulators per wave, 4 waves per SIMD, one "
+                        "workgroup per CU (plh_probe_mfma_f16); `peak` stays the published 2.5 PFLOP/s",
+            },
         },
         "input_projection": {
             "fused": True,

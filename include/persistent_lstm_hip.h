@@ -128,6 +128,14 @@ int plh_set_wait_limit_us(int64_t limit_us);
  * (bindings.cpp:164, persistent_lstm_hip.cu:1684-1695, :1784-1809). */
 int plh_repeat_first_row(const void* in, void* out, int rows, int cols, void* stream);
 
+/*
+ * Diagnostic for benchmarks: the dense fp16 MFMA rate this GPU sustains with
+ * v_mfma_f32_16x16x32_f16 (the recurrent kernels' instruction) on every CU, in TFLOP/s, and the
+ * shader clock during that run, in GHz (about 30 ms on the current device and the null stream;
+ * allocates and frees its own buffers).  No counterpart in the reference, which quotes no peak.
+ */
+int plh_probe_mfma_f16(double* tflops, double* clock_ghz);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpersistent_lstm_hip.so")
 BENCH_PATH = os.path.join(LIB_DIR, "plh_bench")
-SOURCES = ["plh_wavefront.hip", "plh_sliced.hip", "plh_pack.hip", "plh_launch.hip", "plh_capi.hip"]
+SOURCES = ["plh_wavefront.hip", "plh_sliced.hip", "plh_pack.hip", "plh_launch.hip", "plh_probe.hip", "plh_capi.hip"]
 HEADERS = ["plh_internal.h", os.path.join("..", "..", "include", "persistent_lstm_hip.h")]
 
 ARCH = "gfx950"

@@ -344,4 +344,43 @@ int plh_repeat_first_row(const void* in, void* out, int rows, int cols, void* st
   return PLH_OK;
 }
 
+int plh_probe_mfma_f16(double* tflops, double* clock_ghz) {
+  if (!tflops || !clock_ghz) return fail(PLH_ERR_INVALID, "tflops and clock_ghz are required");
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return fail_hip(e, "probe device query");
+  // One workgroup of 16 waves per CU (four waves per SIMD); about 15 ms per launch.
+  const int blocks = cus, iters = 65536;
+  float* out = nullptr;
+  unsigned long long* clk = nullptr;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  std::vector<unsigned long long> h((size_t)2 * blocks);
+  float ms = 0.f;
+  e = hipMalloc(&out, (size_t)blocks * 1024 * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&clk, h.size() * sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipEventCreate(&ev[0]);
+  if (e == hipSuccess) e = hipEventCreate(&ev[1]);
+  if (e == hipSuccess) e = plh::launch_mfma_probe(blocks, iters, out, clk, nullptr);  // warm-up (clocks ramp)
+  if (e == hipSuccess) e = hipEventRecord(ev[0], nullptr);
+  if (e == hipSuccess) e = plh::launch_mfma_probe(blocks, iters, out, clk, nullptr);
+  if (e == hipSuccess) e = hipEventRecord(ev[1], nullptr);
+  if (e == hipSuccess) e = hipEventSynchronize(ev[1]);
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[0], ev[1]);
+  if (e == hipSuccess) e = hipMemcpy(h.data(), clk, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  for (hipEvent_t x : ev)
+    if (x) (void)hipEventDestroy(x);
+  if (out) (void)hipFree(out);
+  if (clk) (void)hipFree(clk);
+  if (e != hipSuccess) return fail_hip(e, "MFMA probe");
+  double cycles = 0.0, ticks = 0.0;
+  for (int b = 0; b < blocks; ++b) {
+    cycles += (double)h[2 * b];
+    ticks += (double)h[2 * b + 1];
+  }
+  *tflops = ms > 0.f ? plh::mfma_probe_flops(blocks, iters) / (ms * 1e-3) / 1e12 : 0.0;
+  *clock_ghz = ticks > 0.0 ? cycles / (ticks * 10.0) : 0.0;  // 100 MHz ticks: 10 ns each
+  return PLH_OK;
+}
+
 }  // extern "C"

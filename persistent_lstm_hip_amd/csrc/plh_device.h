@@ -55,7 +55,7 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Spin (one lane) until *ctr >= need, bounded by `limit` ticks of s_memrealtime (100 MHz), then
 // acquire at agent scope.  Returns 0 if the wait timed out or any workgroup of the grid has failed.
-__device__ int wait_counter(const uint32_t* ctr, uint32_t need, uint32_t* status, uint64_t limit) {
+__device__ __attribute__((unused)) int wait_counter(const uint32_t* ctr, uint32_t need, uint32_t* status, uint64_t limit) {
   uint32_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (v < need) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();

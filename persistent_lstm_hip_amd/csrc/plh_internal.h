@@ -1,5 +1,5 @@
 // plh_internal.h -- declarations shared by the kernel sources (plh_wavefront.hip, plh_sliced.hip,
-// plh_pack.hip, plh_launch.hip) and the C ABI (plh_capi.hip).
+// plh_pack.hip, plh_launch.hip, plh_probe.hip) and the C ABI (plh_capi.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -110,5 +110,11 @@ const void* sliced_kernel(int HP, int wg_tiles);
 // Co-resident workgroups of the persistent kernel on the current device (0 with *err set on error).
 int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err);
 hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s);
+
+// MFMA rate probe (plh_probe.hip): `blocks` workgroups of 16 waves (one per CU), each wave issuing
+// iters x 8 independent v_mfma_f32_16x16x32_f16; out holds blocks x 1024 floats, clk blocks x 2
+// (shader cycles, 100 MHz ticks of the loop).  mfma_probe_flops: the FLOPs of one launch.
+hipError_t launch_mfma_probe(int blocks, int iters, float* out, unsigned long long* clk, hipStream_t s);
+double mfma_probe_flops(int blocks, int iters);
 
 }  // namespace plh

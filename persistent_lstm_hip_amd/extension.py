@@ -64,6 +64,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plh_repeat_first_row.argtypes = [_vp, _vp, _i32, _i32, _vp]
     lib.plh_set_wait_limit_us.restype = _i32
     lib.plh_set_wait_limit_us.argtypes = [_i64]
+    lib.plh_probe_mfma_f16.restype = _i32
+    lib.plh_probe_mfma_f16.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -315,6 +317,14 @@ class NativeLibrary:
         n = _i32(0)
         self._check(self.lib.plh_kernel_timing_read(ctypes.byref(ms), ctypes.byref(n)), "plh_kernel_timing_read")
         return float(ms.value), int(n.value)
+
+    def probe_mfma_f16(self):
+        """(TFLOP/s, shader GHz): dense fp16 MFMA rate of the current device (v_mfma_f32_16x16x32_f16 on
+        every CU) and the clock during that run.  Synchronous, about 30 ms."""
+        tf = ctypes.c_double(0.0)
+        ghz = ctypes.c_double(0.0)
+        self._check(self.lib.plh_probe_mfma_f16(ctypes.byref(tf), ctypes.byref(ghz)), "plh_probe_mfma_f16")
+        return float(tf.value), float(ghz.value)
 
     # ---- reference extension surface (bindings.cpp:154-165) ----------------------------------
     def repeat_first_row(self, inp: torch.Tensor, output_batch_size: int) -> torch.Tensor:

@@ -126,6 +126,11 @@ def test_pack_validates_before_touching_the_device(ext):
     assert p(5, 256 * 8, 4, 24, arr, arr, arr, None, None, None, None, 0, None) == PLH_ERR_UNSUPPORTED
 
 
+def test_mfma_probe_validates_before_touching_the_device(ext):
+    assert ext.lib.plh_probe_mfma_f16(None, None) == PLH_ERR_INVALID
+    assert b"required" in ext.lib.plh_last_error()
+
+
 def test_kernel_timing_arming_without_forwards(ext):
     assert ext.lib.plh_kernel_timing(0) == PLH_OK
     ms, n = ext.kernel_timing_read()

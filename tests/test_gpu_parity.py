@@ -404,3 +404,16 @@ def test_sliced_two_tile_workgroups_ragged_partial_launch(gpu):
     want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
                                     lengths=lengths.numpy())
     assert_close(got.float().cpu().numpy(), want, what="two-tile ragged")
+
+
+def test_mfma_rate_probe(gpu):
+    """The roofline constant checked on the box: the probe's dense fp16 MFMA rate is consistent with
+    the shader clock it measured (one v_mfma_f32_16x16x32_f16 per 16 cycles per SIMD, 1024 SIMDs)
+    and of the order of the published 2.5 PFLOP/s."""
+    _say("MFMA rate probe")
+    tflops, ghz = gpu.probe_mfma_f16()
+    assert 0.5 < ghz < 3.0, ghz
+    per_clock = 16 * 16 * 32 * 2 / 16 * 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    implied = per_clock * ghz * 1e9 / 1e12
+    assert 0.8 * implied < tflops < 1.05 * implied, (tflops, ghz, implied)
+    assert 1000.0 < tflops < 3000.0, tflops

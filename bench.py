@@ -144,9 +144,10 @@ def uniform_batch_protocol(model, dev, warmup: int, steps: int) -> dict:
             "vs_reference_3.08_s": 3.08 / fwd_100}
 
 
-def other_configs(dev, reps: int = 10) -> dict:
+def other_configs(dev, reps: int = 20, warmup: int = 10) -> dict:
     """C3, C4 and C5 (BASELINE.json configs[2..4]) timed the same way as C2 (HIP events, median of
-    `reps` forwards after 3 warm-ups) on their own synthetic models: parity for these is in
+    `reps` forwards after `warmup` untimed ones, so the clock has settled after the previous
+    config) on their own synthetic models: parity for these is in
     tests/test_gpu_parity.py; here only their latency and seq-steps/s are recorded."""
     from persistent_lstm_hip_amd import PersistentLSTMRegressor, StandardLSTMRegressor
 
@@ -164,7 +165,7 @@ def other_configs(dev, reps: int = 10) -> dict:
             steps = int(lengths.sum())
         run = (lambda: model.forward_ragged(x, lengths)) if ragged else (lambda: model(x))  # noqa: E731
         with torch.inference_mode():
-            for _ in range(3):
+            for _ in range(warmup):
                 run()
             ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
             torch.cuda.synchronize()

@@ -417,3 +417,56 @@ def test_mfma_rate_probe(gpu):
     implied = per_clock * ghz * 1e9 / 1e12
     assert 0.8 * implied < tflops < 1.05 * implied, (tflops, ghz, implied)
     assert 1000.0 < tflops < 3000.0, tflops
+
+
+def test_random_geometry_sweep(gpu):
+    """Seeded random geometries through plh_forward: input size, hidden size (both kernel families,
+    padded and unpadded), layers, head size (0 = no head), batch, length, ragged lengths with zeros,
+    initial states and two probe steps.  Every output (head, sequence, final h/c, probed h/c) is
+    checked against the C oracle at the north-star tolerance."""
+    rng = np.random.default_rng(20261202)
+    device = torch.device("cuda")
+    done = 0
+    while done < 48:
+        I = int(rng.integers(1, 41))
+        H = int(rng.integers(1, 129)) if rng.random() < 0.5 else int(rng.integers(129, 513))
+        L = int(rng.integers(1, 5))
+        O = 0 if rng.random() < 0.2 else int(rng.integers(1, 31))
+        B = int(rng.integers(1, 71))
+        T = int(rng.integers(1, 121))
+        if I > (32 if H <= 32 else 64 if H <= 64 else 128 if H <= 128 else 256 if H <= 256 else 512):
+            continue  # input_size above the padded hidden size is outside the supported geometries
+        if B * T * L * 4 * H * (I + H) > 3e8:
+            continue  # keep the oracle to a fraction of a second per case
+        ragged = rng.random() < 0.5
+        with_state = rng.random() < 0.5
+        _say(f"sweep {done}: I={I} H={H} L={L} O={O} B={B} T={T} ragged={ragged} state={with_state}")
+        torch.manual_seed(int(rng.integers(1 << 30)))
+        lstm = torch.nn.LSTM(I, H, L, batch_first=True)
+        head = torch.nn.Linear(H, O) if O else None
+        x = torch.randn(B, T, I, generator=torch.Generator().manual_seed(done))
+        lengths = torch.tensor(rng.integers(0, T + 1, B), dtype=torch.int64) if ragged else None
+        h0 = (0.5 * torch.randn(L, B, H)).half() if with_state else None
+        c0 = (0.5 * torch.randn(L, B, H)).half() if with_state else None
+        probes = sorted(set(int(p) for p in rng.integers(1, T + 1, 2)))
+        params = [[getattr(lstm, f"{n}_l{l}").detach().cuda() for l in range(L)]
+                  for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+        packed = gpu.pack(*params, head.weight.detach().cuda() if head else None,
+                          head.bias.detach().cuda() if head else None)
+        res = gpu.forward(packed, (I, H, L, O), x.to(device, torch.float16), lengths=lengths,
+                          h0=None if h0 is None else h0.to(device), c0=None if c0 is None else c0.to(device),
+                          want_out=O > 0, want_seq=True, want_state=True, probe_steps=probes, check_status=True)
+        want = oracle.lstm_forward(x.numpy(), oracle_layers(lstm), lengths=None if lengths is None else lengths.numpy(),
+                                   h0=None if h0 is None else h0.float().numpy(),
+                                   c0=None if c0 is None else c0.float().numpy(),
+                                   probe_steps=probes, want_seq=True)
+        tag = f"sweep {done}"
+        assert_close(res["out_seq"].float().cpu().numpy(), want["out_seq"], what=f"{tag} out_seq")
+        assert_close(res["h_n"].float().cpu().numpy(), want["h_n"], what=f"{tag} h_n")
+        assert_close(res["c_n"].float().cpu().numpy(), want["c_n"], what=f"{tag} c_n")
+        assert_close(res["probe_h"].cpu().numpy(), want["probe_h"], what=f"{tag} probe_h")
+        assert_close(res["probe_c"].cpu().numpy(), want["probe_c"], what=f"{tag} probe_c")
+        if O:
+            w_head = oracle.linear(want["h_n"][-1], *linear_params(head))
+            assert_close(res["out"].float().cpu().numpy(), w_head, what=f"{tag} head")
+        done += 1

@@ -289,7 +289,8 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   // (uniform, in SGPRs), the thread's byte offset in a VGPR and the word's block offset as the
   // scalar offset, with cache policy sc1 (agent-scope coherent, as agent-scope relaxed atomics).
   // Every offset stays inside the slot.  One-tile workgroups keep the global atomics: the extra
-  // SGPR pressure of the descriptors costs them more than the VGPRs save.
+  // SGPR pressure of the descriptors costs them more than the VGPRs save.  Descriptor word 3 is
+  // 0x00020000: DATA_FORMAT = 32 bit, which untyped buffer accesses need to be non-zero on CDNA.
   auto ring_rs = [&](int i, int t) {
     return __builtin_amdgcn_make_buffer_rsrc(xr(i) + (size_t)(t & 1) * C::kWords, 0, C::kWords * 8, 0x00020000);
   };

@@ -18,7 +18,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpersistent_lstm_hip.so")
 BENCH_PATH = os.path.join(LIB_DIR, "plh_bench")
-SOURCES = ["plh_wavefront.hip", "plh_sliced.hip", "plh_pack.hip", "plh_launch.hip", "plh_probe.hip", "plh_capi.hip"]
+SOURCES = ["plh_wavefront.hip", "plh_sliced.hip", "plh_rec.hip", "plh_pack.hip", "plh_launch.hip", "plh_probe.hip",
+           "plh_capi.hip"]
 HEADERS = ["plh_internal.h", os.path.join("..", "..", "include", "persistent_lstm_hip.h")]
 
 ARCH = "gfx950"
@@ -33,6 +34,9 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-command-line-argument",
 ]
+ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+# rocBLAS computes the layer-sequential path's input projection (one GEMM per layer).
+LINK_FLAGS = ["-L" + ROCM_LIB, "-lrocblas", "-Wl,-rpath," + ROCM_LIB]
 
 
 def hipcc() -> str:
@@ -46,7 +50,7 @@ def build(verbose: bool = False) -> str:
     """Compile every source for gfx950 and link the shared library.  Always recompiles."""
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", tmp]
+    cmd = [hipcc()] + HIPCC_FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + LINK_FLAGS + ["-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

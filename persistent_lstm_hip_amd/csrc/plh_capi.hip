@@ -5,8 +5,10 @@
 // std::runtime_error): here they become PLH_ERR_INVALID / PLH_ERR_HIP plus a message.  Unlike the
 // reference there is no silent fallback: a geometry the kernels do not implement is an error.
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 
 #include <algorithm>
+#include <climits>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -30,7 +32,7 @@ int fail_hip(hipError_t e, const char* what) {
   return fail(PLH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// Co-resident workgroup capacity per (device, HP, tile rows), queried once.
+// Co-resident workgroup capacity per (device, HP, tile rows, path), queried once.
 std::mutex g_cap_mu;
 std::unordered_map<long long, int> g_cap;
 
@@ -38,7 +40,7 @@ int capacity(const plh::Geometry& g, int tile_rows, hipError_t* err) {
   int dev = 0;
   *err = hipGetDevice(&dev);
   if (*err != hipSuccess) return 0;
-  const long long key = ((long long)dev * 4096 + g.HP) * 64 + tile_rows;
+  const long long key = (((long long)dev * 4096 + g.HP) * 64 + tile_rows) * 2 + g.rec;
   {
     std::lock_guard<std::mutex> lk(g_cap_mu);
     auto it = g_cap.find(key);
@@ -54,11 +56,13 @@ int capacity(const plh::Geometry& g, int tile_rows, hipError_t* err) {
 // Launch plan: every (layer, tile, slice) workgroup of one persistent launch must be co-resident.
 // 8-row tiles halve the gate math per workgroup and are used when the whole batch fits one launch
 // with them; otherwise 16-row tiles, and the batch is split into sequential launches if needed.
-// Sliced geometries (HP 256, 512) always use 16-row tiles.
+// Sliced geometries (HP 256, 512) always use 16-row tiles; the layer-sequential one (HP 512) needs only
+// the workgroups of one layer co-resident.
 struct Plan {
   int tile_rows = 16;
   int chunk_rows = 16;
   int wg_tiles = 1;  // sliced: 16-row tiles per workgroup
+  bool rec = false;  // layer-sequential path (plh::as_layer_sequential)
 };
 
 Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
@@ -73,7 +77,7 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
   // Workgroups per layer of one launch; where the launch is large enough, a multiple of 8 of them
   // keeps the XCD-aware mapping available.  A sliced workgroup carries two software-pipelined tiles
   // (where the kernel allows it) only when one tile each would need more than one launch.
-  int groups = cap16 / (g.L * g.slices);
+  int groups = cap16 / (g.rec ? g.slices : g.L * g.slices);
   if (groups >= 8) groups &= ~7;
   groups = std::max(1, groups);
   const int tiles16 = (batch + 15) / 16;
@@ -87,7 +91,7 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
 
 // Plan on the current device; without one (capacity unknown) assume one workgroup per CU of a
 // 256-CU MI355X.
-Plan plan_for(const plh::Geometry& g, int batch, bool need_device, hipError_t* err) {
+Plan plan_path(const plh::Geometry& g, int batch, bool need_device, hipError_t* err) {
   int cap8 = g.slices == 1 ? capacity(g, 8, err) : 0;
   int cap16 = *err == hipSuccess ? capacity(g, 16, err) : 0;
   if (*err != hipSuccess) {
@@ -96,6 +100,23 @@ Plan plan_for(const plh::Geometry& g, int batch, bool need_device, hipError_t* e
     *err = hipSuccess;
   }
   return make_plan(g, batch, cap8, cap16);
+}
+
+// Where both paths exist (HP = 512), the one with the smaller modelled time on an MI355X: the
+// wavefront path runs T + L - 1 steps of about 3.7 us per launch of cap / (16 L) tiles (all
+// layers at once), the layer-sequential path L x T steps of about 4.7 us per launch of up to 512
+// rows plus about 1.1 us of projection GEMM per step and layer.  Small batches fit one wavefront
+// launch and keep it; large ones need several, and the layer-sequential path wins.
+Plan plan_for(const plh::Geometry& g, int batch, int seq_len, bool need_device, hipError_t* err) {
+  const Plan p = plan_path(g, batch, need_device, err);
+  if (!g.rec_ok || *err != hipSuccess) return p;
+  Plan q = plan_path(plh::as_layer_sequential(g), batch, need_device, err);
+  if (*err != hipSuccess) return p;
+  q.rec = true;
+  const long long B = std::max(batch, 1), T = std::max(seq_len, 1);
+  const long long t_wave = 37 * ((B + p.chunk_rows - 1) / p.chunk_rows) * (T + g.L - 1);
+  const long long t_seq = 58 * g.L * ((B + q.chunk_rows - 1) / q.chunk_rows) * T;
+  return t_seq < t_wave ? q : p;
 }
 
 bool geometry(int I, int H, int L, int O, plh::Geometry* g) {
@@ -129,6 +150,55 @@ thread_local KernelTiming g_timing;
 // Bound on inter-workgroup waits of this thread's forwards (plh_set_wait_limit_us).
 constexpr int64_t kDefaultWaitUs = 2000000;
 thread_local int64_t g_wait_us = kDefaultWaitUs;
+
+// rocBLAS handle of the calling thread on each device (the layer-sequential input projection).  A
+// handle is not shared between threads (its stream is per call); handles live until the process ends.
+rocblas_handle blas_handle(int dev, rocblas_status* st) {
+  thread_local std::unordered_map<int, rocblas_handle>* handles = new std::unordered_map<int, rocblas_handle>();
+  auto it = handles->find(dev);
+  if (it != handles->end()) {
+    *st = rocblas_status_success;
+    return it->second;
+  }
+  rocblas_handle h = nullptr;
+  *st = rocblas_create_handle(&h);
+  if (*st != rocblas_status_success) return nullptr;
+  (*handles)[dev] = h;
+  return h;
+}
+
+// gates[t][r][c] = sum_k in[t][r][k] w_ih[c][k] for the T x rows_pad rows of a launch and the 4 HP
+// lane-ordered columns (fp16 operands and result, fp32 accumulation: the reference's torch::matmul
+// of fp16 tensors, persistent_lstm_hip.cu:2988-2991), split so that no call exceeds 32-bit element
+// counts.
+int input_projection(const plh::Geometry& g, const _Float16* w_ih, int K, const _Float16* in, _Float16* gates,
+                     int T, int rows_pad, hipStream_t s) {
+  if (T == 0 || rows_pad == 0) return PLH_OK;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "device query");
+  rocblas_status st;
+  rocblas_handle h = blas_handle(dev, &st);
+  if (st == rocblas_status_success) st = rocblas_set_stream(h, s);
+  if (st != rocblas_status_success)
+    return fail(PLH_ERR_HIP, std::string("rocBLAS handle: ") + rocblas_status_to_string(st));
+  const int m = 4 * g.HP;
+  const int steps = std::max(1, (int)std::min<long long>(T, INT_MAX / ((long long)m * rows_pad)));
+  const float alpha = 1.0f, beta = 0.0f;
+  for (int t0 = 0; t0 < T; t0 += steps) {
+    const int n = std::min(steps, T - t0) * rows_pad;
+    const _Float16* b = in + (size_t)t0 * rows_pad * g.HP;
+    _Float16* c = gates + (size_t)t0 * rows_pad * m;
+    // Column-major view: C (m x n, ldc m) = A^T B with A = w_ih as stored (K x m, lda K) and
+    // B = in (K x n, ldb HP).
+    st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, m, n, K, &alpha, w_ih,
+                         rocblas_datatype_f16_r, K, b, rocblas_datatype_f16_r, g.HP, &beta, c, rocblas_datatype_f16_r,
+                         m, c, rocblas_datatype_f16_r, m, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success)
+      return fail(PLH_ERR_HIP, std::string("rocblas_gemm_ex (input projection): ") + rocblas_status_to_string(st));
+  }
+  return PLH_OK;
+}
 
 }  // namespace
 
@@ -164,11 +234,21 @@ int plh_pack_regressor(int input_size, int hidden_size, int num_layers, int outp
   if (output_size > 0 && !lin_w) return fail(PLH_ERR_INVALID, "lin_w is required when output_size > 0");
   hipStream_t s = (hipStream_t)stream;
   char* base = (char*)packed_dev;
+  size_t wih_off = p.wih;
   for (int l = 0; l < g.L; ++l) {
     if (!w_ih[l] || !w_hh[l]) return fail(PLH_ERR_INVALID, "null weight pointer for layer " + std::to_string(l));
     hipError_t e = plh::launch_pack_layer(g, l, (const _Float16*)w_ih[l], (const _Float16*)w_hh[l],
                                           (_Float16*)(base + p.wpack), s);
     if (e != hipSuccess) return fail_hip(e, "pack_layer launch");
+    if (g.rec_ok) {
+      // The layer-sequential path's operands: W_hh fragments, W_ih as the projection GEMM's A.
+      e = plh::launch_pack_rec_layer(g, l, (const _Float16*)w_hh[l], (_Float16*)(base + p.wrec), s);
+      if (e != hipSuccess) return fail_hip(e, "pack_rec_layer launch");
+      const int K = l == 0 ? g.I : g.H;
+      e = plh::launch_pack_rec_wih(g, (const _Float16*)w_ih[l], K, (_Float16*)(base + wih_off), s);
+      if (e != hipSuccess) return fail_hip(e, "pack_rec_wih launch");
+      wih_off += (size_t)4 * g.HP * K * sizeof(_Float16);
+    }
     e = plh::launch_pack_bias(g, l, (const _Float16*)b_ih[l], b_hh ? (const _Float16*)b_hh[l] : nullptr,
                               (float*)(base + p.bias), s);
     if (e != hipSuccess) return fail_hip(e, "pack_bias launch");
@@ -188,7 +268,8 @@ int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int
     return -1;
   }
   hipError_t err = hipSuccess;
-  const Plan p = plan_for(g, batch, false, &err);
+  const Plan p = plan_for(g, batch, seq_len, false, &err);
+  if (p.rec) g = plh::as_layer_sequential(g);
   return (int64_t)plh::workspace_layout(g, seq_len, p.chunk_rows, p.tile_rows).total;
 }
 
@@ -209,10 +290,12 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   hipStream_t s = (hipStream_t)stream;
 
   hipError_t err = hipSuccess;
-  const Plan plan = plan_for(g, batch, true, &err);
+  const Plan plan = plan_for(g, batch, seq_len, true, &err);
   if (err != hipSuccess) return fail_hip(err, "occupancy query");
-  if (capacity(g, 16, &err) < g.L * g.slices)
-    return fail(PLH_ERR_UNSUPPORTED, "the device cannot hold the " + std::to_string(g.L * g.slices) +
+  if (plan.rec) g = plh::as_layer_sequential(g);
+  const int tile_wgs = g.rec ? g.slices : g.L * g.slices;
+  if (capacity(g, 16, &err) < tile_wgs)
+    return fail(PLH_ERR_UNSUPPORTED, "the device cannot hold the " + std::to_string(tile_wgs) +
                                          " workgroups of one batch tile co-resident (layers = " +
                                          std::to_string(g.L) + ")");
   const int chunk_rows = plan.chunk_rows;
@@ -235,7 +318,7 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   std::memset(&a, 0, sizeof(a));
   a.x = (const _Float16*)x;
   a.lengths = lengths;
-  a.wpack = (const _Float16*)(pk + p.wpack);
+  a.wpack = (const _Float16*)(pk + (g.rec ? p.wrec : p.wpack));
   a.bias = (const float*)(pk + p.bias);
   a.wlin = (const float*)(pk + p.wlin);
   a.blin = (const float*)(pk + p.blin);
@@ -273,7 +356,39 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     a.wg_tiles = plan.wg_tiles;
     a.ntile = (a.ntile + a.wg_tiles - 1) / a.wg_tiles * a.wg_tiles;
     a.rows_pad = a.ntile * plan.tile_rows;
-    a.xcd_map = (g.slices > 1 ? (g.L * a.ntile / a.wg_tiles) % 8 : a.ntile % 8) == 0 ? 1 : 0;
+    a.xcd_map = ((g.slices > 1 && !g.rec) ? (g.L * a.ntile / a.wg_tiles) % 8 : a.ntile % 8) == 0 ? 1 : 0;
+    if (g.rec) {
+      // Layer by layer: x of this chunk into xs slot 0; per layer the input projection of every
+      // step (one GEMM), the exchange ring cleared (tags restart at 1), and the recurrent kernel,
+      // whose h sequence goes to the other xs slot as the next layer's input.
+      _Float16* xs[2] = {(_Float16*)(ws + w.xs),
+                         (_Float16*)(ws + w.xs) + (size_t)seq_len * chunk_rows * g.HP};
+      if (row0 == 0) {
+        err = plh::launch_zero_u32(status, 1, s);
+        if (err != hipSuccess) return fail_hip(err, "status reset");
+        if (timed) {
+          err = hipEventRecord(g_timing.ev[2 * g_timing.used], s);
+          if (err != hipSuccess) return fail_hip(err, "timing event");
+        }
+      }
+      err = plh::launch_rec_input(g, a, xs[0], s);
+      if (err != hipSuccess) return fail_hip(err, "input transpose");
+      const _Float16* wih = (const _Float16*)(pk + p.wih);
+      a.gates = (const _Float16*)(ws + w.gates);
+      for (int l = 0; l < g.L; ++l) {
+        const int K = l == 0 ? g.I : g.H;
+        const int rc = input_projection(g, wih, K, xs[l & 1], (_Float16*)(ws + w.gates), seq_len, a.rows_pad, s);
+        if (rc != PLH_OK) return rc;
+        wih += (size_t)4 * g.HP * K;
+        err = plh::launch_zero_u32((uint32_t*)a.xring, w.xring_words * 2, s);
+        if (err != hipSuccess) return fail_hip(err, "exchange ring reset");
+        a.layer = l;
+        a.hout = l + 1 < g.L ? xs[(l + 1) & 1] : nullptr;
+        err = plh::launch_recurrent(g, a, s);
+        if (err != hipSuccess) return fail_hip(err, "persistent LSTM launch");
+      }
+      continue;
+    }
     // x of this launch's rows into xp; status (first launch), counters and, when sliced, the
     // exchange ring (tags restart at 1) cleared: one launch ahead of the persistent one
     err = plh::launch_forward_prologue(g, a, row0 == 0 ? status : nullptr, s);

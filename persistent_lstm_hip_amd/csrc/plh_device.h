@@ -105,5 +105,51 @@ struct Sliced {
   static __host__ __device__ constexpr int member_of(int w) { return (w >> 2) * kKsp + (w & (kKsp - 1)); }
   static __host__ __device__ constexpr int wave_of(int g, int e) { return (e / kKsp) * 4 + g * kKsp + e % kKsp; }
 };
+
+// Work split of the layer-sequential recurrent kernel (padded H = 512, plh_rec.hip): the input
+// projection comes precomputed, so a workgroup holds only W_hh rows, for HS = 64 hidden units, and
+// S = 8 workgroups serve a 16-row tile.  Wave w serves unit group w % 4 (16 units) with the K half
+// w / 4 of h_{t-1} (8 K-chunks of 32 x 4 gates = 128 VGPRs).
+template <int HP>
+struct Rec {
+  static constexpr int kS = 8;            // workgroups per 16-row tile
+  static constexpr int kHs = HP / kS;     // hidden units per workgroup
+  static constexpr int kKch = HP / 32;    // K chunks of h
+  static constexpr int kKcw = kKch / 2;   // K chunks per wave
+  static constexpr int kWords = HP * 8;   // tagged words of one step's h of a 16-row tile
+  static_assert(kHs == 64, "four 16-unit groups per workgroup");
+};
+
+// ---- tagged exchange of h among the workgroups of a tile (plh_sliced.hip, plh_rec.hip) ----
+
+__device__ __forceinline__ uint64_t tag_word(_Float16 a, _Float16 b, uint32_t tag) {
+  union { _Float16 h[2]; uint32_t u; } v;
+  v.h[0] = a;
+  v.h[1] = b;
+  return (uint64_t)v.u | ((uint64_t)tag << 32);
+}
+
+__device__ __forceinline__ uint32_t word_tag(uint64_t w) { return (uint32_t)(w >> 32); }
+
+__device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup -> (layer, tile, slice).  With xcd_map the S slices of a (layer, tile) share an XCD.
+__device__ __forceinline__ void sliced_coords(int b, int ntile, int S, int xcd_map, int& layer, int& tile,
+                                              int& slice) {
+  int grp;
+  if (xcd_map) {
+    const int j = b >> 3;
+    slice = j % S;
+    grp = (j / S) * 8 + (b & 7);
+  } else {
+    slice = b % S;
+    grp = b / S;
+  }
+  layer = grp / ntile;
+  tile = grp % ntile;
+}
+
 }  // namespace
 }  // namespace plh

@@ -17,8 +17,12 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 // i = f = o = 0.5, g = 0 and their c and h stay exactly 0: padding never changes real outputs.
 struct Geometry {
   int I, H, L, O;
-  int HP;      // padded hidden size: 32, 64, 128 (one workgroup per layer and tile) or 256, 512 (sliced)
-  int slices;  // workgroups per (layer, tile): 1, or HP / 64 (HP = 256) and HP / 32 (HP = 512)
+  int HP;      // padded hidden size: 32, 64, 128 (one workgroup per layer and tile), 256 (sliced) or
+               // 512 (layer-sequential)
+  int slices;  // workgroups per (layer, tile): 1, 4 (HP = 256), 16 (HP = 512) or 8 (layer-sequential)
+  int rec_ok;  // HP = 512: the layer-sequential path exists (its weights are packed too)
+  int rec;     // this forward runs layer by layer: input projection as a GEMM, recurrent kernel
+               // holding W_hh alone (make_geometry leaves 0; as_layer_sequential sets it)
   int max_wg_tiles;  // 16-row tiles a sliced workgroup can carry (2 at HP = 256, software-pipelined)
   int waves;   // waves per workgroup: HP / 16 (one per 16 hidden units) or 8 when sliced
   int kci;     // input-part K chunks of 32 for layers >= 1 (= HP / 32)
@@ -28,6 +32,8 @@ struct Geometry {
 
 // Fills *g; returns false (with the reason) for geometries the kernels do not implement.
 bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why);
+// g (rec_ok) switched to the layer-sequential path.
+Geometry as_layer_sequential(const Geometry& g);
 
 // Byte offsets of the packed-weight blob (all 256-byte aligned).
 struct PackedLayout {
@@ -36,6 +42,10 @@ struct PackedLayout {
   size_t bias;   // f32 [L][4][HP]: b_ih + b_hh
   size_t wlin;   // f32 [O][HP]
   size_t blin;   // f32 [O]
+  size_t wrec;   // rec_ok: f16 W_hh fragments of the layer-sequential kernel, [L][8 slices][8 waves][8
+                 // chunks][4 gates][64 lanes][8]
+  size_t wih;    // rec_ok: f16 W_ih of every layer as the projection GEMM's A operand, [4 HP][I], then
+                 // [4 HP][H] per layer: rows permuted to the kernel's lane order
   size_t total;
 };
 PackedLayout packed_layout(const Geometry& g);
@@ -49,8 +59,13 @@ PackedLayout packed_layout(const Geometry& g);
 //   hseq     f16x8 [L-1][ntile][T][kci][4][R]      h of layers 0..L-2 in B-fragment order
 //   xring    u64 [L][ntile][2][HP * 8]             sliced geometries only: per-step exchange of h
 //                                                  among the slices of a (layer, tile), tagged words
+// Layer-sequential geometries (one layer per launch) use instead of xp and hseq:
+//   gates    f16 [T][rows][4 HP]                   one layer's input projection x_t W_ih^T, columns
+//                                                  in the recurrent kernel's lane order
+//   xs       f16 [2][T][rows][HP]                  layer inputs/outputs, alternating (x in slot 0)
+// and an xring of one layer.
 struct WorkspaceLayout {
-  size_t status, counters, xp, hseq, xring, total;
+  size_t status, counters, xp, hseq, xring, gates, xs, total;
   size_t xring_words;  // u64 words of xring (0 unless sliced)
   int chunk_rows;  // batch rows per persistent launch (co-residency bound), multiple of tile_rows
   int tile_rows;   // batch rows per workgroup: 8 or 16
@@ -87,6 +102,10 @@ struct ForwardArgs {
   int xcd_map;                  // 1: keep a tile's layer chain on one XCD
   uint64_t wait_ticks;          // bound on one inter-workgroup wait, in s_memrealtime ticks (100 MHz)
   int wg_tiles;                 // sliced kernels: 16-row tiles per workgroup (1 or 2); ntile is a multiple
+  // layer-sequential kernel (one layer per launch):
+  int layer;                    // the layer this launch runs
+  const _Float16* gates;        // [T][rows_pad][4 HP] input projection of that layer (no bias), lane order
+  _Float16* hout;               // [T][rows_pad][HP] its h sequence, the next layer's input (null: last layer)
 };
 
 hipError_t launch_pack_layer(const Geometry& g, int layer, const _Float16* w_ih, const _Float16* w_hh,
@@ -110,6 +129,14 @@ const void* sliced_kernel(int HP, int wg_tiles);
 // Co-resident workgroups of the persistent kernel on the current device (0 with *err set on error).
 int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err);
 hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s);
+
+// Layer-sequential path (plh_rec.hip): W_hh fragments of one layer, x of a launch's rows into
+// xs slot 0 ([T][rows_pad][HP], zero past the launch's rows), and the recurrent kernel of a.layer.
+hipError_t launch_pack_rec_layer(const Geometry& g, int layer, const _Float16* w_hh, _Float16* wpack, hipStream_t s);
+hipError_t launch_rec_input(const Geometry& g, const ForwardArgs& a, _Float16* xs0, hipStream_t s);
+// W_ih ([4H][K]) of one layer as the projection GEMM's A operand ([4 HP][K], lane-ordered rows).
+hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, _Float16* dst, hipStream_t s);
+const void* rec_kernel(int HP);
 
 // MFMA rate probe (plh_probe.hip): `blocks` workgroups of 16 waves (one per CU), each wave issuing
 // iters x 8 independent v_mfma_f32_16x16x32_f16; out holds blocks x 1024 floats, clk blocks x 2

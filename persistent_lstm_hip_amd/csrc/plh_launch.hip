@@ -32,6 +32,8 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
   g->L = L;
   g->O = O;
   g->HP = HP;
+  g->rec_ok = HP == 512 ? 1 : 0;
+  g->rec = 0;
   g->slices = HP == 256 ? Sliced<256>::kS : HP == 512 ? Sliced<512>::kS : 1;
   g->max_wg_tiles = HP == 256 ? 2 : 1;
   g->waves = g->slices > 1 ? 8 : HP / 16;
@@ -39,6 +41,14 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
   g->kc = 2 * g->kci;
   g->g_in0 = (I + 7) / 8;
   return true;
+}
+
+Geometry as_layer_sequential(const Geometry& g) {
+  Geometry r = g;
+  r.rec = 1;
+  r.slices = Rec<512>::kS;
+  r.max_wg_tiles = 1;
+  return r;
 }
 
 static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -56,6 +66,11 @@ PackedLayout packed_layout(const Geometry& g) {
   off = align256(off + (size_t)g.O * g.HP * sizeof(float));
   p.blin = off;
   off = align256(off + (size_t)g.O * sizeof(float));
+  // The layer-sequential kernel's W_hh alone (half of the above) and the projection GEMM's W_ih.
+  p.wrec = off;
+  if (g.rec_ok) off = align256(off + (size_t)g.L * (g.HP / 16) * g.kci * 4 * 64 * 8 * sizeof(_Float16));
+  p.wih = off;
+  if (g.rec_ok) off = align256(off + (size_t)4 * g.HP * (g.I + (size_t)(g.L - 1) * g.H) * sizeof(_Float16));
   p.total = off;
   return p;
 }
@@ -69,14 +84,24 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   w.status = 0;
   w.counters = 256;
   w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile);
+  if (g.rec) {
+    w.hseq = w.xring = w.xp;
+    w.xring_words = ntile * 2 * g.HP * 8;
+    w.gates = align256(w.xring + w.xring_words * sizeof(uint64_t));
+    w.xs = align256(w.gates + (size_t)seq_len * chunk_rows * 4 * g.HP * sizeof(_Float16));
+    w.total = align256(w.xs + (size_t)2 * seq_len * chunk_rows * g.HP * sizeof(_Float16));
+    return w;
+  }
   w.hseq = align256(w.xp + ntile * seq_len * g.g_in0 * tile_rows * 16);
   w.xring = align256(w.hseq + (size_t)(g.L - 1) * ntile * seq_len * g.kci * frag_bytes);
   w.xring_words = g.slices > 1 ? (size_t)g.L * ntile * 2 * g.HP * 8 : 0;
   w.total = align256(w.xring + w.xring_words * sizeof(uint64_t));
+  w.gates = w.xs = w.total;
   return w;
 }
 
 static const void* recurrent_kernel(const Geometry& g, int tile_rows, bool ragged, int wg_tiles = 1) {
+  if (g.rec) return tile_rows == 16 && wg_tiles == 1 ? rec_kernel(g.HP) : nullptr;
   if (g.slices > 1) return tile_rows == 16 ? sliced_kernel(g.HP, wg_tiles) : nullptr;
   return wavefront_kernel(g.HP, tile_rows, ragged);
 }
@@ -107,8 +132,9 @@ hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t
   if (!fn || a.wg_tiles < 1 || a.ntile % a.wg_tiles) return hipErrorInvalidValue;
   ForwardArgs args = a;
   void* params[] = {&args};
-  return hipLaunchCooperativeKernel(fn, dim3(a.L * a.ntile / a.wg_tiles * g.slices), dim3(g.waves * 64), params, 0,
-                                    s);
+  // One layer per launch (layer-sequential) or every layer of the chunk at once.
+  const unsigned grid = g.rec ? a.ntile * g.slices : a.L * a.ntile / a.wg_tiles * g.slices;
+  return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(g.waves * 64), params, 0, s);
 }
 
 }  // namespace plh

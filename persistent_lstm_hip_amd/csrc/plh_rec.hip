@@ -1,0 +1,416 @@
+// plh_rec.hip -- the layer-sequential path for padded H = 512 on CDNA4 (gfx950).
+//
+// With [W_ih | W_hh] resident (plh_sliced.hip) a layer of H = 512 needs 16 workgroups per 16-row
+// tile, so a 256-CU device covers 64 rows of all layers per launch.  Here each layer's input
+// projection for all T steps is one GEMM (x_t W_ih^T, fp16 in and out with fp32 accumulation, as
+// the reference's torch::matmul of fp16 tensors; issued by the host, plh_capi.hip) and the
+// persistent kernel below keeps only W_hh resident: 8 workgroups ("slices") per 16-row tile, 64
+// hidden units each, so one launch covers 512 rows of one layer.  The layers run one after another.
+//   * the GEMM's output columns are in lane order: W_ih's rows are permuted (and padded to 4 HP) at
+//     pack time so that the 8 projections one lane needs per step (4 gates x 2 units) are 16
+//     contiguous bytes, one load, issued two steps ahead;
+//   * wave w of a slice holds the i, f, g, o rows of W_hh for unit group w % 4 (16 units) and the
+//     K half w / 4 of h_{t-1}: 8 K-chunks x 4 gates of MFMA A fragments (128 VGPRs);
+//   * per step each wave computes its partial gate sums from h_{t-1} in LDS (32 MFMAs), the two
+//     K halves meet in LDS, and the two waves of a group split its 16 units x 16 rows (two units
+//     per lane), adding the bias and the precomputed input projection;
+//   * the slices exchange h_t every step through the tagged-word ring of plh_sliced.hip (same
+//     writer order, words and protocol); h_t also goes to the next layer's GEMM input.
+//
+// Reference behaviour restated (mantuoluozk/persistent_lstm_hip): the generic path's per-layer
+// input projection followed by a persistent recurrence (persistent_lstm_hip.cu:2923-3181), gate
+// order i, f, g, o and the c/h recurrence of persistent_lstm_reference.cpp:21-35.
+#include "plh_device.h"
+
+namespace plh {
+namespace {
+
+// [L][S][8 waves][8 chunks][4 gates][64 lanes][8]: wave w of slice s holds W_hh rows of unit group
+// w % 4 and K half w / 4.
+template <int HP>
+__global__ void pack_rec_kernel(const _Float16* __restrict__ w_hh, int H, _Float16* __restrict__ dst) {
+  using C = Rec<HP>;
+  const size_t total = (size_t)C::kS * 8 * C::kKcw * 4 * 64 * 8;
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= total) return;
+  const int j = e & 7;
+  const int lane = (e >> 3) & 63;
+  const int q = (e >> 9) & 3;
+  const int kc = (int)((e >> 11) & 7);
+  const int wv = (int)((e >> 14) & 7);
+  const int sl = (int)(e >> 17);
+  const int u = sl * C::kHs + (wv & 3) * 16 + (lane & 15);
+  const int k = ((wv >> 2) * C::kKcw + kc) * 32 + (lane >> 4) * 8 + j;
+  dst[e] = (u < H && k < H) ? w_hh[((size_t)q * H + u) * H + k] : (_Float16)0.0f;
+}
+
+// Column of the input projection that lane `lane` of wave `wave` in slice `slice` reads as element
+// 2 q + j: gate q of unit slice * 64 + (wave % 4) * 16 + (lane / 16) * 4 + 2 (wave / 4) + j.
+__host__ __device__ constexpr int rec_gate_col(int slice, int wave, int kgx) {
+  return ((slice * 8 + wave) * 4 + kgx) * 8;
+}
+
+// W_ih ([4H][K], torch layout) as the GEMM's A operand [4 HP][K] with rows in lane order (the
+// inverse of rec_gate_col) and zero rows for padded units.
+__global__ void pack_rec_wih_kernel(const _Float16* __restrict__ w_ih, int H, int HP, int K,
+                                    _Float16* __restrict__ dst) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (size_t)4 * HP * K) return;
+  const int col = (int)(e / K), k = (int)(e % K);
+  const int q = (col & 7) >> 1, j = col & 1, kgx = (col >> 3) & 3, wave = (col >> 5) & 7, slice = col >> 8;
+  const int u = slice * 64 + (wave & 3) * 16 + kgx * 4 + 2 * (wave >> 2) + j;
+  dst[e] = u < H ? w_ih[((size_t)q * H + u) * K + k] : (_Float16)0.0f;
+}
+
+// x rows [row0, row_end) into [T][rows_pad][HP] (the first GEMM's input, K = I columns used).
+__global__ void rec_input_kernel(const _Float16* __restrict__ x, int T, int I, int row0, int row_end, int rows_pad,
+                                 int HP, _Float16* __restrict__ xs) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (size_t)T * rows_pad * I) return;
+  const int i = (int)(e % I);
+  const size_t tb = e / I;
+  const int b = (int)(tb % rows_pad);
+  const int t = (int)(tb / rows_pad);
+  const int r = row0 + b;
+  xs[tb * HP + i] = r < row_end ? x[((size_t)r * T + t) * I + i] : (_Float16)0.0f;
+}
+
+template <int HP>
+__global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
+  using C = Rec<HP>;
+  constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch, KCW = C::kKcw;
+  constexpr int NT = 512, FV = 64, NW = C::kWords / NT;
+  static_assert(C::kWords % NT == 0, "whole tagged words per thread");
+
+  __shared__ f16x8 hbuf[KCH * FV];  // h_{t-1} of all HP units, fragment order
+  __shared__ f32x4 part[8][4][64];  // partial gate sums of every wave
+  __shared__ float2 s_bias[4][HS / 2];
+  __shared__ int s_fail;
+  __shared__ int s_tlen;
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int unused_layer, tile, slice;
+  sliced_coords(blockIdx.x, a.ntile, S, a.xcd_map, unused_layer, tile, slice);
+  const int layer = a.layer;
+  const int g = wave & 3, e = wave >> 2;  // unit group, K half
+  const int en = lane & 15, kgx = lane >> 4;
+  // This lane's units eu, eu + 1 of row en: elements 2e, 2e + 1 of lane `lane` of the group's D
+  // fragments (units 4 kgx + i, row en).
+  const int eu = slice * HS + g * 16 + kgx * 4 + 2 * e;
+  const int b = tile * 16 + en;  // row within this launch
+  const int grow = a.row0 + b;
+  const bool row_ok = grow < a.row_end;
+  const bool last = a.hout == nullptr;
+
+  if (threadIdx.x == 0) {
+    s_tlen = 0;
+    // A failed wait of an earlier layer's launch (this forward's status word) fails this one too,
+    // so that the head is poisoned whichever layer timed out.
+    s_fail = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+  }
+  __syncthreads();
+  int len = 0;
+  if (row_ok) {
+    len = a.lengths ? a.lengths[grow] : a.T;
+    len = len < 0 ? 0 : (len > a.T ? a.T : len);
+  }
+  if (wave == 0 && lane < 16) atomicMax(&s_tlen, len);
+  __syncthreads();
+  // Steps of this tile: its longest row.  Workgroup-uniform values read from LDS go through
+  // readfirstlane, so that the loop's exits are uniform branches the compiler leaves unstructured.
+  const int Tt = __builtin_amdgcn_readfirstlane(s_tlen);
+
+  f16x8 w[KCW][4];
+  {
+    const f16x8* wp =
+        reinterpret_cast<const f16x8*>(a.wpack) + (size_t)((layer * S + slice) * 8 + wave) * KCW * 4 * 64 + lane;
+#pragma unroll
+    for (int kc = 0; kc < KCW; ++kc)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
+  }
+  // The resident weights complete here (otherwise the compiler keeps them "possibly outstanding"
+  // and waits for every global access in flight before the step loop's MFMAs).
+  __builtin_amdgcn_s_waitcnt(0);
+  for (int idx = threadIdx.x; idx < 4 * HS / 2; idx += NT) {
+    const int q = idx / (HS / 2), up = idx % (HS / 2);
+    const float* bp = a.bias + ((size_t)layer * 4 + q) * HP + slice * HS + 2 * up;
+    s_bias[q][up] = float2{bp[0], bp[1]};
+  }
+
+  float c[2];
+  _Float16 hcur[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int u = eu + j;
+    const bool v = row_ok && u < a.H;
+    const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
+    c[j] = (v && a.c0) ? (float)a.c0[si] : 0.0f;
+    hcur[j] = (v && a.h0) ? a.h0[si] : (_Float16)0.0f;
+  }
+  // h_{-1} of all units of the tile's rows into hbuf (fragment order)
+  for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) {
+    const int kc = idx / FV, l = idx % FV;
+    const int gr = a.row0 + tile * 16 + (l & 15);
+    const int k0 = kc * 32 + (l >> 4) * 8;
+    f16x8 v = {};
+    if (a.h0 && gr < a.row_end) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (k0 + j < a.H) v[j] = a.h0[((size_t)layer * a.B + gr) * a.H + k0 + j];
+    }
+    hbuf[idx] = v;
+  }
+  __syncthreads();  // hbuf and s_bias complete before the first step (or the head, if no step runs)
+
+  // Input projection of step min(t, Tt - 1) for this lane's row and units, bias excluded: element
+  // 2 q + j is gate q of unit eu + j.  Padded units read zero columns and padded rows zero inputs.
+  // One unconditional 16-byte load (a load under an exec branch makes the compiler wait for it
+  // together with the ring poll), consumed two steps after it is issued.
+  const _Float16* gsrc = a.gates + b * (size_t)(4 * HP) + rec_gate_col(slice, wave, kgx);
+  auto gload = [&](int t) -> f16x8 {
+    return *reinterpret_cast<const f16x8*>(gsrc + (size_t)(t < Tt ? t : Tt - 1) * a.rows_pad * (4 * HP));
+  };
+
+  uint64_t* ring = a.xring + (size_t)tile * 2 * C::kWords;
+  const int woff = (slice * 8 + wave) * 64 + lane;  // writer order [slice][wave][lane]
+  // LDS destination (u32 index into hbuf) of the r-th word this thread gathers.
+  auto gdst = [&](int r) -> int {
+    const int wd = threadIdx.x + r * NT;
+    const int sl = wd / 512, wv_ = (wd / 64) % 8, ln = wd % 64;
+    const int eu_ = sl * HS + (wv_ & 3) * 16 + (ln >> 4) * 4 + 2 * (wv_ >> 2);
+    return ((eu_ >> 3) * 16 + (ln & 15)) * 4 + ((eu_ & 7) >> 1);
+  };
+
+  int probe_i = 0;
+  // Probe steps live in SGPRs (a VGPR loaded in the loop would put a vmcnt(0) on every step).
+  int probe_next = a.n_probe > 0 ? __builtin_amdgcn_readfirstlane(a.probe_steps[0]) : -1;
+  auto write_probe = [&](int pi) {
+    if (!row_ok) return;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int u = eu + j;
+      if (u < a.H) {
+        const size_t o = (((size_t)pi * a.L + layer) * a.B + grow) * a.H + u;
+        a.probe_h[o] = (float)hcur[j];
+        a.probe_c[o] = c[j];
+      }
+    }
+  };
+
+  uint64_t wv[NW];
+  // One step: h_{t-1} in hbuf -> h_t in hbuf; gp holds the input projection of step t and is
+  // reloaded with that of step t + 2; gq holds that of step t + 1.  Returns false if a wait failed.
+  auto step = [&](int t, f16x8& gp, f16x8& gq) -> bool {
+    // Partial gate sums of this wave's K half of h_{t-1}.
+    {
+      const f16x8* src = hbuf + e * KCW * FV + lane;
+      f32x4 acc[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < KCW; ++kc) {
+        const f16x8 bv = src[kc * FV];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], bv, acc[q], 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) part[wave][q][lane] = acc[q];
+    }
+    lds_barrier();
+
+    // Gate math: bias + both K halves + the input projection.
+    const bool live = t < len;
+    {
+      float z[4][2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float2 bv = s_bias[q][(eu - slice * HS) >> 1];
+        z[q][0] = bv.x + (float)gp[2 * q];
+        z[q][1] = bv.y + (float)gp[2 * q + 1];
+#pragma unroll
+        for (int ee = 0; ee < 2; ++ee) {
+          const float2 v = reinterpret_cast<const float2*>(&part[ee * 4 + g][q][lane])[e];
+          z[q][0] += v.x;
+          z[q][1] += v.y;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float cn = c[j], hn;
+        lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn, hn);
+        c[j] = live ? cn : c[j];
+        hcur[j] = live ? (_Float16)hn : hcur[j];
+      }
+    }
+
+    // h_t: the tagged word for the sibling slices first, then the first poll of all words of step
+    // t, and only then the stores and loads off the critical path (the next layer's input, the
+    // output sequence, probes, the next step's input projection): loads and stores retire in issue
+    // order, so the poll waits for nothing issued after it.
+    __hip_atomic_store(ring + (size_t)(t & 1) * C::kWords + woff, tag_word(hcur[0], hcur[1], (uint32_t)t + 1u),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t* src = ring + (size_t)(t & 1) * C::kWords + threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < NW; ++r) wv[r] = load_agent_u64(src + r * NT);
+    if (!last) {
+      union { _Float16 h[2]; uint32_t u; } v;
+      v.h[0] = hcur[0];
+      v.h[1] = hcur[1];
+      *reinterpret_cast<uint32_t*>(a.hout + ((size_t)t * a.rows_pad + b) * HP + eu) = v.u;
+    } else if (a.out_seq && row_ok) {
+      _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (eu + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
+    }
+    if (t + 1 == probe_next) {
+      write_probe(probe_i);
+      ++probe_i;
+      probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
+    }
+
+    // Gather h_t of every slice: re-poll the words whose tag is not t + 1 yet (bounded wait).
+    const uint32_t want = (uint32_t)t + 1u;
+    uint64_t t0 = 0;
+    for (int spin = 0;; ++spin) {
+      bool ready = true;
+#pragma unroll
+      for (int r = 0; r < NW; ++r) ready = ready && word_tag(wv[r]) == want;
+      if (ready) break;
+      if (spin == 0) {
+        t0 = __builtin_amdgcn_s_memrealtime();
+      } else if ((spin & 15) == 0) {
+        if (__hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+          s_fail = 1;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
+          __hip_atomic_fetch_or(a.status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          s_fail = 1;
+          break;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < NW; ++r)
+        if (word_tag(wv[r]) != want) wv[r] = load_agent_u64(src + r * NT);
+    }
+    // gq's load was issued before this step's poll, so it has completed (loads retire in order);
+    // the empty asm tells the compiler, which would otherwise wait for every load in flight at
+    // the next step's gate math.  Then the projection of step t + 2, issued after the poll (the
+    // compiler waits for every load in flight where the poll's retry path joins).
+    asm volatile("" : "+v"(gq));
+    gp = gload(t + 2);
+    uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf);
+#pragma unroll
+    for (int r = 0; r < NW; ++r) hb32[gdst(r)] = (uint32_t)wv[r];
+    lds_barrier();
+    return __builtin_amdgcn_readfirstlane(s_fail) == 0;
+  };
+
+  // Two steps per iteration, so each projection buffer keeps its registers (no copies of loads in
+  // flight, which would wait for them).
+  f16x8 g0 = {}, g1 = {};
+  if (Tt > 0) g0 = gload(0);
+  if (Tt > 1) g1 = gload(1);
+  // Nothing in flight at the loop entry: otherwise the compiler merges a pending g0 into the loop
+  // header and waits for every load at each step's gate math, the one of step t + 1 included.
+  wait_vmem_all();
+  // The loop's back edge follows the odd step only: at the top, g0's load has been waited for by
+  // the odd step's poll (loads retire in order), so the gate math waits for nothing in flight.
+  bool ok = __builtin_amdgcn_readfirstlane(s_fail) == 0;
+  for (int t = 0; ok && t < Tt; t += 2) {
+    if (!(ok = step(t, g0, g1)) || t + 1 >= Tt) break;
+    if (!(ok = step(t + 1, g1, g0))) break;
+  }
+
+  if (!ok) {
+    // A wait failed (the status word records it): poison this tile's head outputs and leave.
+    if (last && slice == 0 && a.out) {
+      for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
+        const int gr = a.row0 + tile * 16 + idx / a.O;
+        if (gr < a.row_end) a.out[(size_t)gr * a.O + idx % a.O] = (_Float16)__builtin_nanf("");
+      }
+    }
+    return;
+  }
+
+  // Steps past the tile's longest row were never visited: their output sequence is zero.
+  if (last && a.out_seq && row_ok) {
+    for (int t = Tt; t < a.T; ++t) {
+      _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (eu + j < a.H) dst[j] = (_Float16)0.0f;
+    }
+  }
+  // ... and the next layer's input there is the frozen state (its rows are frozen as well).
+  while (probe_i < a.n_probe) {
+    write_probe(probe_i);
+    ++probe_i;
+  }
+  if (row_ok) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int u = eu + j;
+      if (u < a.H) {
+        const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
+        if (a.h_n) a.h_n[si] = hcur[j];
+        if (a.c_n) a.c_n[si] = (_Float16)c[j];
+      }
+    }
+  }
+  // Linear head (last layer, first slice) on the full final h held in hbuf.
+  if (last && slice == 0 && a.out) {
+    for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
+      const int rr = idx / a.O, o = idx % a.O;
+      const int gr = a.row0 + tile * 16 + rr;
+      if (gr >= a.row_end) continue;
+      const _Float16* hf = reinterpret_cast<const _Float16*>(hbuf);
+      const float* wr = a.wlin + (size_t)o * HP;
+      float s0 = 0.f, s1 = 0.f;
+      for (int k8 = 0; k8 < HP; k8 += 8) {
+        const f16x8 hv = *reinterpret_cast<const f16x8*>(hf + frag_index<16>(rr, k8));
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          s0 = fmaf((float)hv[j], wr[k8 + j], s0);
+          s1 = fmaf((float)hv[j + 1], wr[k8 + j + 1], s1);
+        }
+      }
+      a.out[(size_t)gr * a.O + o] = (_Float16)(a.blin[o] + (s0 + s1));
+    }
+  }
+}
+
+inline unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+hipError_t launch_pack_rec_layer(const Geometry& g, int layer, const _Float16* w_hh, _Float16* wpack, hipStream_t s) {
+  if (g.HP != 512) return hipErrorInvalidValue;
+  using C = Rec<512>;
+  const size_t per_layer = (size_t)C::kS * 8 * C::kKcw * 4 * 64 * 8;
+  hipLaunchKernelGGL(pack_rec_kernel<512>, blocks_for(per_layer, 256), 256, 0, s, w_hh, g.H, wpack + layer * per_layer);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, _Float16* dst, hipStream_t s) {
+  const size_t n = (size_t)4 * g.HP * K;
+  hipLaunchKernelGGL(pack_rec_wih_kernel, blocks_for(n, 256), 256, 0, s, w_ih, g.H, g.HP, K, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_rec_input(const Geometry& g, const ForwardArgs& a, _Float16* xs0, hipStream_t s) {
+  const size_t n = (size_t)a.T * a.rows_pad * g.I;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(rec_input_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, g.I, a.row0, a.row_end, a.rows_pad,
+                     g.HP, xs0);
+  return hipGetLastError();
+}
+
+const void* rec_kernel(int HP) {
+  return HP == 512 ? reinterpret_cast<const void*>(&lstm_rec_kernel<512>) : nullptr;
+}
+
+}  // namespace plh

@@ -34,35 +34,6 @@
 namespace plh {
 namespace {
 
-__device__ __forceinline__ uint64_t tag_word(_Float16 a, _Float16 b, uint32_t tag) {
-  union { _Float16 h[2]; uint32_t u; } v;
-  v.h[0] = a;
-  v.h[1] = b;
-  return (uint64_t)v.u | ((uint64_t)tag << 32);
-}
-
-__device__ __forceinline__ uint32_t word_tag(uint64_t w) { return (uint32_t)(w >> 32); }
-
-__device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Workgroup -> (layer, tile, slice).  With xcd_map the S slices of a (layer, tile) share an XCD.
-__device__ __forceinline__ void sliced_coords(int b, int ntile, int S, int xcd_map, int& layer, int& tile,
-                                              int& slice) {
-  int grp;
-  if (xcd_map) {
-    const int j = b >> 3;
-    slice = j % S;
-    grp = (j / S) * 8 + (b & 7);
-  } else {
-    slice = b % S;
-    grp = b / S;
-  }
-  layer = grp / ntile;
-  tile = grp % ntile;
-}
-
 // NTI 16-row tiles per workgroup.  With NTI = 2 the two tiles are software-pipelined: a tile's
 // gather of h_t (issued right after its own words were stored) is completed in the middle of the
 // other tile's step, after that tile's gate math and before its stores, so the exchange latency

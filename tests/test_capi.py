@@ -67,6 +67,11 @@ def test_packed_bytes_closed_form(ext):
                            (5, 256, 4, 24, 256), (5, 200, 2, 3, 256), (5, 512, 4, 24, 512), (7, 400, 1, 1, 512)]:
         wp = L * (HP // 16) * (HP // 16) * 4 * 64 * 16
         want = a(wp) + a(L * 4 * HP * 4) + a(O * HP * 4) + a(O * 4)
+        if HP == 512:
+            # both paths' operands: the layer-sequential kernel's W_hh fragments (half of the above) and
+            # W_ih of every layer as its projection GEMM's operand, padded to 4 HP rows ([4HP][I], then
+            # [4HP][H])
+            want += a(wp // 2) + a(4 * HP * (I + (L - 1) * H) * 2)
         assert ext.packed_bytes(I, H, L, O) == want
     with pytest.raises(ValueError):
         ext.packed_bytes(5, 1000, 4, 24)
@@ -88,15 +93,33 @@ def test_sliced_workspace_layout(ext):
     # the slices exchange h every step: L * tiles * 2 * (HP * 8) words of 8 bytes.  Without a device the
     # plan assumes 256 co-resident workgroups: 256 / (L * 4 slices) = 16 workgroups per layer at
     # HP = 256, each carrying two 16-row tiles (the whole 512-row batch), and 256 / (L * 16) = 4
-    # one-tile workgroups at HP = 512.
+    # one-tile workgroups at HP = 512 (a 64-row batch: one launch, where the wavefront path is the
+    # faster one).
     L, T = 4, 1000
-    for H, tiles in ((256, 32), (512, 4)):
+    for H, tiles, batch in ((256, 32, 512), (512, 4, 64)):
         rows = tiles * 16
-        b = ext.workspace_bytes(5, H, L, 24, 512, T)
+        b = ext.workspace_bytes(5, H, L, 24, batch, T)
         handoff = (L - 1) * rows * T * H * 2
         ring = L * tiles * 2 * H * 8 * 8
         xp = rows * T * 8 * 2  # x of the launch: one 8-wide K group (I = 5) per row and step
         assert handoff + ring + xp <= b < handoff + ring + xp + (1 << 12)
+
+
+def test_layer_sequential_workspace_layout(ext):
+    # HP = 512 with a batch that needs several wavefront launches (8 of 64 rows here) runs layer by
+    # layer: 8 workgroups per 16-row tile hold one layer's W_hh, so 256 / 8 = 32 tiles (512 rows) fit
+    # one launch.  The workspace holds one layer's input projection for every
+    # step (fp16 [T][rows][4HP]), two alternating fp16 layer-input buffers [T][rows][HP] and one
+    # layer's exchange ring (tiles * 2 * HP * 8 words of 8 bytes).
+    L, T, H = 4, 1000, 512
+    rows = 512
+    b = ext.workspace_bytes(5, H, L, 24, 512, T)
+    gates = T * rows * 4 * H * 2
+    xs = 2 * T * rows * H * 2
+    ring = (rows // 16) * 2 * H * 8 * 8
+    assert gates + xs + ring <= b < gates + xs + ring + (1 << 12)
+    # a padded H (400 -> 512) is sized by HP throughout
+    assert ext.workspace_bytes(5, 400, L, 24, 512, T) == b
 
 
 def test_forward_validates_before_touching_the_device(ext):

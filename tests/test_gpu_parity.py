@@ -257,7 +257,8 @@ def test_large_batches_use_16_row_tiles_and_split_launches(gpu, B, T):
 
 @pytest.mark.parametrize("H,rows_checked", [(256, 512), (512, 48)])
 def test_large_hidden_c3_c4(gpu, H, rows_checked):
-    """C3 (H256) and C4 (H512): 4 layers, B512, T1000, served by the sliced kernel in several launches.
+    """C3 (H256) and C4 (H512): 4 layers, B512, T1000.  C3 runs the sliced kernel (two tiles per
+    workgroup), C4 the layer-sequential path (one 512-row launch per layer).
 
     Output vs torch fp32 on `rows_checked` rows spread over every launch; h and c after 1, 100 and
     1000 steps vs the oracle on rows of the first and the last launch.
@@ -310,6 +311,41 @@ def test_sliced_persistent_lstm_dropin_with_state(gpu):
     want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear),
                                     lengths=lengths.numpy())
     assert_close(got, want, what="sliced ragged")
+
+
+@pytest.mark.parametrize("H", [512, 300])
+def test_layer_sequential_path_dropin_with_state_and_ragged(gpu, H):
+    """H512-bucket batches that need several wavefront launches run layer by layer (input projection
+    as one fp16 GEMM per layer, then the W_hh-only recurrent kernel): 1100 rows are three launches of
+    up to 512 rows.  PersistentLSTM with h0/c0, the full output sequence and the final state vs torch
+    fp32; then ragged lengths (zeros included, unsorted) through the regressor vs the oracle."""
+    I, L, B, T = 24, 2, 1100, 7
+    _say(f"layer-sequential H={H} B={B} T={T}")
+    torch.manual_seed(31)
+    lstm = torch.nn.LSTM(I, H, L, batch_first=True).eval()
+    x = make_x(B, T, I, seed=32)
+    g = torch.Generator().manual_seed(33)
+    h0 = 0.5 * torch.randn(L, B, H, generator=g)
+    c0 = 0.5 * torch.randn(L, B, H, generator=g)
+    with torch.inference_mode():
+        want_out, (want_h, want_c) = lstm(x, (h0, c0))
+    mod = PersistentLSTM.from_native_module(lstm).to("cuda").half()
+    out, (h, c) = mod(x.to("cuda", torch.float16), (h0.cuda().half(), c0.cuda().half()))
+    gpu.check_status(torch.device("cuda"))
+    assert_close(out.float().cpu().numpy(), want_out.numpy(), what="layer-sequential out seq")
+    assert_close(h.float().cpu().numpy(), want_h.numpy(), what="layer-sequential h_n")
+    assert_close(c.float().cpu().numpy(), want_c.numpy(), what="layer-sequential c_n")
+    lengths = torch.randint(0, T + 1, (B,), generator=g)
+    lengths[5] = 0
+    lengths[700] = T
+    native = make_regressor(I, H, L, 6)
+    model = _gpu_model(native)
+    got = model.forward_ragged(x.to("cuda", torch.float16), lengths).float().cpu().numpy()
+    gpu.check_status(torch.device("cuda"))
+    rows = np.r_[0:40, 500:530, 1060:1100]  # every launch, the partial last one included
+    want = oracle.regressor_forward(x.numpy()[rows], oracle_layers(native.lstm), *linear_params(native.linear),
+                                    lengths=lengths.numpy()[rows])
+    assert_close(got[rows], want, what="layer-sequential ragged")
 
 
 @pytest.mark.parametrize("H,B", [(128, 16), (256, 16), (256, 600)])

@@ -200,6 +200,14 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   };
 
   uint64_t wv[NW];
+  // The next layer's input: h_t of this slice's 64 units x 16 rows, written a step later from
+  // hbuf as 128 contiguous 16-byte runs (each row's 128 bytes whole) instead of 4-byte pieces.
+  constexpr int kCopyThreads = HS * 16 / 8;
+  const int copy_row = threadIdx.x & 15, copy_k8 = slice * (HS / 8) + (threadIdx.x >> 4) % (HS / 8);
+  const int copy_src = copy_k8 * 16 + copy_row;  // f16x8 index of (row, units 8 copy_k8 ..) in hbuf
+  auto copy_out = [&](int t, const f16x8& v) {
+    *reinterpret_cast<f16x8*>(a.hout + ((size_t)t * a.rows_pad + tile * 16 + copy_row) * HP + copy_k8 * 8) = v;
+  };
   // One step: h_{t-1} in hbuf -> h_t in hbuf; gp holds the input projection of step t and is
   // reloaded with that of step t + 2; gq holds that of step t + 1.  Returns false if a wait failed.
   auto step = [&](int t, f16x8& gp, f16x8& gq) -> bool {
@@ -218,6 +226,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) part[wave][q][lane] = acc[q];
     }
+    // h_{t-1} of this slice's units, 16 bytes per thread of waves 0-1, read before the barrier
+    // after which the step's gather overwrites hbuf; stored below as the next layer's input.
+    f16x8 hcp = {};
+    if (!last && threadIdx.x < kCopyThreads) hcp = hbuf[copy_src];
     lds_barrier();
 
     // Gate math: bias + both K halves + the input projection.
@@ -255,10 +267,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
 #pragma unroll
     for (int r = 0; r < NW; ++r) wv[r] = load_agent_u64(src + r * NT);
     if (!last) {
-      union { _Float16 h[2]; uint32_t u; } v;
-      v.h[0] = hcur[0];
-      v.h[1] = hcur[1];
-      *reinterpret_cast<uint32_t*>(a.hout + ((size_t)t * a.rows_pad + b) * HP + eu) = v.u;
+      if (threadIdx.x < kCopyThreads && t > 0) copy_out(t - 1, hcp);
     } else if (a.out_seq && row_ok) {
       _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
 #pragma unroll
@@ -324,6 +333,8 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     if (!(ok = step(t, g0, g1)) || t + 1 >= Tt) break;
     if (!(ok = step(t + 1, g1, g0))) break;
   }
+  // The last step's h (in hbuf after its gather) as the next layer's input.
+  if (ok && !last && Tt > 0 && threadIdx.x < kCopyThreads) copy_out(Tt - 1, hbuf[copy_src]);
 
   if (!ok) {
     // A wait failed (the status word records it): poison this tile's head outputs and leave.

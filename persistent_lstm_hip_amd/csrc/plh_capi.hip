@@ -106,13 +106,18 @@ Plan plan_path(const plh::Geometry& g, int batch, bool need_device, hipError_t* 
 // wavefront path runs T + L - 1 steps of about 3.7 us per launch of cap / (16 L) tiles (all
 // layers at once), the layer-sequential path L x T steps of about 4.7 us per launch of up to 512
 // rows plus about 1.1 us of projection GEMM per step and layer.  Small batches fit one wavefront
-// launch and keep it; large ones need several, and the layer-sequential path wins.
+// launch and keep it; large ones need several, and the layer-sequential path wins.  Its workspace
+// holds a layer's projections for every step (~3 MB per step at 512 rows); sequences that would
+// need more than kMaxSeqWorkspace stay on the wavefront path (~0.2 MB per step).
+constexpr size_t kMaxSeqWorkspace = (size_t)24 << 30;
 Plan plan_for(const plh::Geometry& g, int batch, int seq_len, bool need_device, hipError_t* err) {
   const Plan p = plan_path(g, batch, need_device, err);
   if (!g.rec_ok || *err != hipSuccess) return p;
-  Plan q = plan_path(plh::as_layer_sequential(g), batch, need_device, err);
+  const plh::Geometry gr = plh::as_layer_sequential(g);
+  Plan q = plan_path(gr, batch, need_device, err);
   if (*err != hipSuccess) return p;
   q.rec = true;
+  if (plh::workspace_layout(gr, seq_len, q.chunk_rows, q.tile_rows).total > kMaxSeqWorkspace) return p;
   const long long B = std::max(batch, 1), T = std::max(seq_len, 1);
   const long long t_wave = 37 * ((B + p.chunk_rows - 1) / p.chunk_rows) * (T + g.L - 1);
   const long long t_seq = 58 * g.L * ((B + q.chunk_rows - 1) / q.chunk_rows) * T;

@@ -120,6 +120,12 @@ def test_layer_sequential_workspace_layout(ext):
     assert gates + xs + ring <= b < gates + xs + ring + (1 << 12)
     # a padded H (400 -> 512) is sized by HP throughout
     assert ext.workspace_bytes(5, 400, L, 24, 512, T) == b
+    # sequences whose projections would exceed 24 GiB stay on the wavefront path (64 rows per launch:
+    # x, the (L-1)-layer hand-off and the ring), whatever the batch
+    T = 10000
+    b = ext.workspace_bytes(5, H, L, 24, 512, T)
+    wave = 64 * T * 8 * 2 + (L - 1) * 64 * T * H * 2 + L * 4 * 2 * H * 8 * 8
+    assert wave <= b < wave + (1 << 12)
 
 
 def test_forward_validates_before_touching_the_device(ext):

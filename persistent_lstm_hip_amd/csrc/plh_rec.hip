@@ -177,12 +177,22 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   const int woff = (slice * 8 + wave) * 64 + lane;  // writer order [slice][wave][lane]
   // LDS destination (u32 index into hbuf) of the r-th word this thread gathers: words 2 thread and
   // 2 thread + 1 of each 1024-word block.
+  // A workgroup gathers the 7 sibling slices' words (its own go to hbuf from registers): load k of
+  // a thread reads words 2 (tid % 256) and 2 (tid % 256) + 1 of sibling block 2 k + tid / 256 (the
+  // blocks in slice order without this workgroup's own), so waves 0-3 issue 4 loads, waves 4-7 3.
+  const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
+  const int nld = half ? 3 : 4;
+  auto sib = [&](int k) {
+    const int r = 2 * k + half;
+    return r + (r >= slice ? 1 : 0);
+  };
   auto gdst = [&](int r) -> int {
-    const int wd = (r >> 1) * 2 * NT + threadIdx.x * 2 + (r & 1);
-    const int sl = wd / 512, wv_ = (wd / 64) % 8, ln = wd % 64;
-    const int eu_ = sl * HS + (wv_ & 3) * 16 + (ln >> 4) * 4 + 2 * (wv_ >> 2);
+    const int wq = 2 * (threadIdx.x & 255) + (r & 1);  // word within the sibling's block
+    const int wv_ = wq / 64, ln = wq % 64;
+    const int eu_ = sib(r >> 1) * HS + (wv_ & 3) * 16 + (ln >> 4) * 4 + 2 * (wv_ >> 2);
     return ((eu_ >> 3) * 16 + (ln & 15)) * 4 + ((eu_ & 7) >> 1);
   };
+  const int own_dst = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's pair in hbuf
 
   int probe_i = 0;
   // Probe steps live in SGPRs (a VGPR loaded in the loop would put a vmcnt(0) on every step).
@@ -264,7 +274,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // order, so the poll waits for nothing issued after it.
     __hip_atomic_store(ring + (size_t)(t & 1) * C::kWords + woff, tag_word(hcur[0], hcur[1], (uint32_t)t + 1u),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // The poll reads two adjacent words per 16-byte buffer load with cache policy sc1 (what
+    // The poll reads two adjacent words of a sibling per 16-byte buffer load with cache policy sc1 (what
     // agent-scope relaxed atomics compile to): a descriptor of the ring slot in SGPRs (word 3
     // 0x00020000: DATA_FORMAT = 32 bit, which untyped buffer accesses need on CDNA), the thread's
     // byte offset in one VGPR, the block offset as the scalar offset, every offset inside the slot.
@@ -275,12 +285,20 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)(t & 1) * C::kWords, 0, C::kWords * 8, 0x00020000);
     auto pload = [&](int p) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16u, p * NT * 16, 16);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (threadIdx.x & 255) * 16u, sib(p) * 512 * 8, 16);
       wv[2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
       wv[2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
     };
 #pragma unroll
-    for (int p = 0; p < NW / 2; ++p) pload(p);
+    for (int p = 0; p < NW / 2; ++p)
+      if (p < nld) pload(p);
+    // This lane's own pair of h_t (no step-t reader of hbuf is left after the first barrier).
+    {
+      union { _Float16 h[2]; uint32_t u; } v;
+      v.h[0] = hcur[0];
+      v.h[1] = hcur[1];
+      reinterpret_cast<uint32_t*>(hbuf)[own_dst] = v.u;
+    }
     if (!last) {
       if (threadIdx.x < kCopyThreads && t > 0) copy_out(t - 1, hcp);
     } else if (a.out_seq && row_ok) {
@@ -301,7 +319,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < NW; ++r) ready = ready && word_tag(wv[r]) == want;
+      for (int r = 0; r < NW; ++r) ready = ready && ((r >> 1) >= nld || word_tag(wv[r]) == want);
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -319,7 +337,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
       for (int p = 0; p < NW / 2; ++p)
-        if (word_tag(wv[2 * p]) != want || word_tag(wv[2 * p + 1]) != want) pload(p);
+        if (p < nld && (word_tag(wv[2 * p]) != want || word_tag(wv[2 * p + 1]) != want)) pload(p);
     }
     // gq's load was issued before this step's poll, so it has completed (loads retire in order);
     // the empty asm tells the compiler, which would otherwise wait for every load in flight at
@@ -329,7 +347,8 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     gp = gload(t + 2);
     uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf);
 #pragma unroll
-    for (int r = 0; r < NW; ++r) hb32[gdst(r)] = (uint32_t)wv[r];
+    for (int r = 0; r < NW; ++r)
+      if ((r >> 1) < nld) hb32[gdst(r)] = (uint32_t)wv[r];
     lds_barrier();
     return __builtin_amdgcn_readfirstlane(s_fail) == 0;
   };

@@ -348,6 +348,29 @@ def test_layer_sequential_path_dropin_with_state_and_ragged(gpu, H):
     assert_close(got[rows], want, what="layer-sequential ragged")
 
 
+@pytest.mark.parametrize("T", [1, 2, 3])
+def test_layer_sequential_short_sequences(gpu, T):
+    """Layer-sequential path with 1, 2 and 3 steps (the kernel runs two steps per loop iteration and
+    loads the projection two steps ahead, clamped to the last step): 600 rows are a 512-row launch
+    and an 88-row one (6 tiles, no XCD mapping).  Full output sequence and final state vs torch fp32."""
+    I, H, L, B = 5, 512, 2, 600
+    _say(f"layer-sequential short T={T}")
+    torch.manual_seed(41)
+    lstm = torch.nn.LSTM(I, H, L, batch_first=True).eval()
+    x = make_x(B, T, I, seed=42)
+    g = torch.Generator().manual_seed(43)
+    h0 = 0.5 * torch.randn(L, B, H, generator=g)
+    c0 = 0.5 * torch.randn(L, B, H, generator=g)
+    with torch.inference_mode():
+        want_out, (want_h, want_c) = lstm(x, (h0, c0))
+    mod = PersistentLSTM.from_native_module(lstm).to("cuda").half()
+    out, (h, c) = mod(x.to("cuda", torch.float16), (h0.cuda().half(), c0.cuda().half()))
+    gpu.check_status(torch.device("cuda"))
+    assert_close(out.float().cpu().numpy(), want_out.numpy(), what=f"T={T} out seq")
+    assert_close(h.float().cpu().numpy(), want_h.numpy(), what=f"T={T} h_n")
+    assert_close(c.float().cpu().numpy(), want_c.numpy(), what=f"T={T} c_n")
+
+
 @pytest.mark.parametrize("H,B", [(128, 16), (256, 16), (256, 600)])
 def test_wait_timeout_is_reported_and_recovers(gpu, H, B):
     """A forced 1 us wait bound: the next layer's first hand-off wait cannot be met, so the kernel sets

@@ -79,8 +79,8 @@ template <int HP>
 __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   using C = Rec<HP>;
   constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch, KCW = C::kKcw;
-  constexpr int NT = 512, FV = 64, NW = C::kWords / NT;
-  static_assert(C::kWords % NT == 0, "whole tagged words per thread");
+  constexpr int NT = 512, FV = 64, NW = 4;  // packed words each thread gathers per step (at most)
+  constexpr int PW = C::kWords / 2;          // packed words of one step's h of a tile (4 fp16 each)
 
   __shared__ f16x8 hbuf[KCH * FV];  // h_{t-1} of all HP units, fragment order
   __shared__ f32x4 part[8][4][64];  // partial gate sums of every wave
@@ -173,26 +173,47 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     return *reinterpret_cast<const f16x8*>(gsrc + (size_t)(t < Tt ? t : Tt - 1) * a.rows_pad * (4 * HP));
   };
 
-  uint64_t* ring = a.xring + (size_t)tile * 2 * C::kWords;
-  const int woff = (slice * 8 + wave) * 64 + lane;  // writer order [slice][wave][lane]
-  // LDS destination (u32 index into hbuf) of the r-th word this thread gathers: words 2 thread and
-  // 2 thread + 1 of each 1024-word block.
-  // A workgroup gathers the 7 sibling slices' words (its own go to hbuf from registers): load k of
-  // a thread reads words 2 (tid % 256) and 2 (tid % 256) + 1 of sibling block 2 k + tid / 256 (the
-  // blocks in slice order without this workgroup's own), so waves 0-3 issue 4 loads, waves 4-7 3.
-  const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
-  const int nld = half ? 3 : 4;
+  // Packed exchange.  A word carries 4 fp16 of one row: the pair of a lane with even kgx (units
+  // 4 kgx + 2e, +1) and that of its partner lane + 16 (the next 4 units), and a 4-bit step tag in
+  // bit 14 of each fp16.  That bit is clear in every h a step computes (|h| <= 1 < 2); NaN and
+  // infinity, the only other values with it set, travel as +-1.5 (never an h) and come back as NaN.
+  // The bit is cleared in every value sent, so the tag is always intact; rows of length 0 keep their
+  // h0, which may use it: their exchanged values only feed their own (frozen) rows and are restored
+  // from h0 before they are read as results.  Half the bytes of one word per pair with a 32-bit
+  // tag.  Words are in writer order [slice][wave][32].
+  uint64_t* ring = a.xring + (size_t)tile * 2 * C::kWords;  // a slot of PW words per step parity
+  const int pwoff = (slice * 8 + wave) * 32 + (kgx >> 1) * 16 + en;  // this lane's word (even kgx)
+  // A workgroup gathers the 7 sibling slices' words (its own pairs go to hbuf from registers): load
+  // k of a thread reads words 2 (tid % 128) and 2 (tid % 128) + 1 of sibling block 4 k + tid / 128
+  // (the blocks in slice order without this workgroup's own), so waves 0-5 issue 2 loads, 6-7 one.
+  const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7);
+  const int nld = quarter < 3 ? 2 : 1;
   auto sib = [&](int k) {
-    const int r = 2 * k + half;
+    const int r = 4 * k + quarter;
     return r + (r >= slice ? 1 : 0);
   };
+  // LDS destination (u32 index into hbuf) of the first pair of the r-th word this thread gathers;
+  // the second pair (4 units on) is 2 further.
   auto gdst = [&](int r) -> int {
-    const int wq = 2 * (threadIdx.x & 255) + (r & 1);  // word within the sibling's block
-    const int wv_ = wq / 64, ln = wq % 64;
-    const int eu_ = sib(r >> 1) * HS + (wv_ & 3) * 16 + (ln >> 4) * 4 + 2 * (wv_ >> 2);
-    return ((eu_ >> 3) * 16 + (ln & 15)) * 4 + ((eu_ & 7) >> 1);
+    const int wq = 2 * (threadIdx.x & 127) + (r & 1);  // word within the sibling's block
+    const int wv_ = wq >> 5, en_ = wq & 15, kgx_ = 2 * ((wq >> 4) & 1);
+    const int eu_ = sib(r >> 1) * HS + (wv_ & 3) * 16 + kgx_ * 4 + 2 * (wv_ >> 2);
+    return ((eu_ >> 3) * 16 + en_) * 4 + ((eu_ & 7) >> 1);
   };
   const int own_dst = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's pair in hbuf
+  auto enc_half = [](_Float16 h) -> uint32_t {
+    const uint32_t b = __builtin_bit_cast(uint16_t, h);
+    return (b & 0x7C00u) == 0x7C00u ? (b & 0x8000u) | 0x3E00u : b & 0xBFFFu;
+  };
+  auto dec_pair = [](uint32_t v) -> uint32_t {
+    uint32_t x = v & 0xBFFFBFFFu;
+    if ((x & 0x7FFFu) == 0x3E00u) x |= 0x7E00u;
+    if ((x & 0x7FFF0000u) == 0x3E000000u) x |= 0x7E000000u;
+    return x;
+  };
+  auto ptag = [](uint64_t w) -> uint32_t {
+    return (uint32_t)(((w >> 14) & 1u) | ((w >> 29) & 2u) | ((w >> 44) & 4u) | ((w >> 59) & 8u));
+  };
 
   int probe_i = 0;
   // Probe steps live in SGPRs (a VGPR loaded in the loop would put a vmcnt(0) on every step).
@@ -272,8 +293,17 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // t, and only then the stores and loads off the critical path (the next layer's input, the
     // output sequence, probes, the next step's input projection): loads and stores retire in issue
     // order, so the poll waits for nothing issued after it.
-    __hip_atomic_store(ring + (size_t)(t & 1) * C::kWords + woff, tag_word(hcur[0], hcur[1], (uint32_t)t + 1u),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Tags of successive writes to a slot (steps t - 2, t) differ, and none is 0 (the cleared ring).
+    const uint32_t want = (uint32_t)((t >> 1) % 15) + 1u;
+    {
+      const uint32_t mine = enc_half(hcur[0]) | (enc_half(hcur[1]) << 16);
+      const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
+      const uint64_t tagbits = ((uint64_t)(want & 1u) << 14) | ((uint64_t)((want >> 1) & 1u) << 30) |
+                               ((uint64_t)((want >> 2) & 1u) << 46) | ((uint64_t)((want >> 3) & 1u) << 62);
+      if ((kgx & 1) == 0)
+        __hip_atomic_store(ring + (size_t)(t & 1) * PW + pwoff, ((uint64_t)mine | ((uint64_t)other << 32)) | tagbits,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     // The poll reads two adjacent words of a sibling per 16-byte buffer load with cache policy sc1 (what
     // agent-scope relaxed atomics compile to): a descriptor of the ring slot in SGPRs (word 3
     // 0x00020000: DATA_FORMAT = 32 bit, which untyped buffer accesses need on CDNA), the thread's
@@ -283,9 +313,9 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // different steps, and a load is repeated until both are current).  Half the load
     // instructions of 8-byte atomic loads: C4 21.5 -> 20.0 ms.
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)(t & 1) * C::kWords, 0, C::kWords * 8, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)(t & 1) * PW, 0, PW * 8, 0x00020000);
     auto pload = [&](int p) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (threadIdx.x & 255) * 16u, sib(p) * 512 * 8, 16);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (threadIdx.x & 127) * 16u, sib(p) * (PW / 8) * 8, 16);
       wv[2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
       wv[2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
     };
@@ -313,13 +343,12 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
     }
 
-    // Gather h_t of every slice: re-poll the words whose tag is not t + 1 yet (bounded wait).
-    const uint32_t want = (uint32_t)t + 1u;
+    // Gather h_t of every slice: re-poll the words whose tag is not step t's yet (bounded wait).
     uint64_t t0 = 0;
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < NW; ++r) ready = ready && ((r >> 1) >= nld || word_tag(wv[r]) == want);
+      for (int r = 0; r < NW; ++r) ready = ready && ((r >> 1) >= nld || ptag(wv[r]) == want);
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -337,7 +366,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
       for (int p = 0; p < NW / 2; ++p)
-        if (p < nld && (word_tag(wv[2 * p]) != want || word_tag(wv[2 * p + 1]) != want)) pload(p);
+        if (p < nld && (ptag(wv[2 * p]) != want || ptag(wv[2 * p + 1]) != want)) pload(p);
     }
     // gq's load was issued before this step's poll, so it has completed (loads retire in order);
     // the empty asm tells the compiler, which would otherwise wait for every load in flight at
@@ -348,7 +377,11 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf);
 #pragma unroll
     for (int r = 0; r < NW; ++r)
-      if ((r >> 1) < nld) hb32[gdst(r)] = (uint32_t)wv[r];
+      if ((r >> 1) < nld) {
+        const int d = gdst(r);
+        hb32[d] = dec_pair((uint32_t)wv[r]);
+        hb32[d + 2] = dec_pair((uint32_t)(wv[r] >> 32));
+      }
     lds_barrier();
     return __builtin_amdgcn_readfirstlane(s_fail) == 0;
   };
@@ -367,6 +400,24 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   for (int t = 0; ok && t < Tt; t += 2) {
     if (!(ok = step(t, g0, g1)) || t + 1 >= Tt) break;
     if (!(ok = step(t + 1, g1, g0))) break;
+  }
+  // Rows of length 0 keep their h0, which the packed exchange may not carry intact: restore their
+  // h in hbuf before it is read as a result (the last copy-out, the head).
+  if (ok && a.lengths && Tt > 0) {
+    for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) {
+      const int kc = idx / FV, l = idx % FV;
+      const int gr = a.row0 + tile * 16 + (l & 15);
+      if (gr >= a.row_end || a.lengths[gr] > 0) continue;
+      const int k0 = kc * 32 + (l >> 4) * 8;
+      f16x8 v = {};
+      if (a.h0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (k0 + j < a.H) v[j] = a.h0[((size_t)layer * a.B + gr) * a.H + k0 + j];
+      }
+      hbuf[idx] = v;
+    }
+    __syncthreads();
   }
   // The last step's h (in hbuf after its gather) as the next layer's input.
   if (ok && !last && Tt > 0 && threadIdx.x < kCopyThreads) copy_out(Tt - 1, hbuf[copy_src]);

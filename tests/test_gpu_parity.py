@@ -371,6 +371,53 @@ def test_layer_sequential_short_sequences(gpu, T):
     assert_close(c.float().cpu().numpy(), want_c.numpy(), what=f"T={T} c_n")
 
 
+def test_layer_sequential_zero_lengths_large_state_and_nan(gpu):
+    """The layer-sequential exchange packs 4 fp16 per word with the step tag in bit 14 of each (clear
+    in every computed h).  Rows of length 0 keep h0, which may use that bit (|h0| >= 2 here): their
+    results must still be exact, and no wait may hang on a clobbered tag.  A NaN input row must give
+    NaN (NaN travels as a reserved code) and leave the other rows untouched."""
+    I, H, L, O, B, T = 5, 512, 2, 7, 600, 2  # 600 rows, 2 steps: the layer-sequential path's choice
+    _say("layer-sequential zero lengths, |h0| >= 2, NaN row")
+    device = torch.device("cuda")
+    torch.manual_seed(51)
+    lstm = torch.nn.LSTM(I, H, L, batch_first=True)
+    head = torch.nn.Linear(H, O)
+    x = torch.randn(B, T, I, generator=torch.Generator().manual_seed(52))
+    g = torch.Generator().manual_seed(53)
+    lengths = torch.randint(0, T + 1, (B,), generator=g)
+    lengths[:20] = 0
+    lengths[300:310] = 0
+    h0 = (3.0 * torch.randn(L, B, H, generator=g)).half()
+    c0 = (0.5 * torch.randn(L, B, H, generator=g)).half()
+    params = [[getattr(lstm, f"{n}_l{l}").detach().cuda() for l in range(L)]
+              for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+    packed = gpu.pack(*params, head.weight.detach().cuda(), head.bias.detach().cuda())
+    res = gpu.forward(packed, (I, H, L, O), x.to(device, torch.float16), lengths=lengths, h0=h0.to(device),
+                      c0=c0.to(device), want_out=True, want_seq=True, want_state=True, probe_steps=[1, 2],
+                      check_status=True)
+    rows = np.r_[0:40, 295:320, 560:600]
+    want = oracle.lstm_forward(x.numpy()[rows], oracle_layers(lstm), lengths=lengths.numpy()[rows],
+                               h0=h0.float().numpy()[:, rows], c0=c0.float().numpy()[:, rows],
+                               probe_steps=[1, 2], want_seq=True)
+    assert_close(res["out_seq"].float().cpu().numpy()[rows], want["out_seq"], what="out_seq")
+    assert_close(res["h_n"].float().cpu().numpy()[:, rows], want["h_n"], what="h_n")
+    assert_close(res["c_n"].float().cpu().numpy()[:, rows], want["c_n"], what="c_n")
+    assert_close(res["probe_h"].cpu().numpy()[:, :, rows], want["probe_h"], what="probe_h")
+    w_head = oracle.linear(want["h_n"][-1], *linear_params(head))
+    assert_close(res["out"].float().cpu().numpy()[rows], w_head, what="head (h0 rows restored)")
+    # a NaN input on one full-length row
+    xn = x.clone()
+    xn[7, 1, 2] = float("nan")
+    full = torch.full((B,), T, dtype=torch.int64)
+    res_n = gpu.forward(packed, (I, H, L, O), xn.to(device, torch.float16), lengths=full, want_out=True,
+                        want_seq=False, want_state=True, check_status=True)
+    res_c = gpu.forward(packed, (I, H, L, O), x.to(device, torch.float16), lengths=full, want_out=True,
+                        want_seq=False, want_state=True, check_status=True)
+    assert torch.isnan(res_n["out"][7].float()).all() and torch.isnan(res_n["h_n"][:, 7].float()).all()
+    others = np.r_[0:7, 8:B]
+    np.testing.assert_array_equal(res_n["out"].cpu().numpy()[others], res_c["out"].cpu().numpy()[others])
+
+
 @pytest.mark.parametrize("H,B", [(128, 16), (256, 16), (256, 600)])
 def test_wait_timeout_is_reported_and_recovers(gpu, H, B):
     """A forced 1 us wait bound: the next layer's first hand-off wait cannot be met, so the kernel sets

@@ -116,11 +116,13 @@ struct Rec {
   static constexpr int kHs = HP / kS;     // hidden units per workgroup
   static constexpr int kKch = HP / 32;    // K chunks of h
   static constexpr int kKcw = kKch / 2;   // K chunks per wave
-  static constexpr int kWords = HP * 8;   // tagged words of one step's h of a 16-row tile
+  static constexpr int kWords = HP * 8;   // ring words reserved per step slot of a tile (the packed
+                                          // words of one step take half)
   static_assert(kHs == 64, "four 16-unit groups per workgroup");
 };
 
-// ---- tagged exchange of h among the workgroups of a tile (plh_sliced.hip, plh_rec.hip) ----
+// ---- tagged exchange of h among the workgroups of a tile (plh_sliced.hip; plh_rec.hip shares
+// sliced_coords and packs its words itself) ----
 
 __device__ __forceinline__ uint64_t tag_word(_Float16 a, _Float16 b, uint32_t tag) {
   union { _Float16 h[2]; uint32_t u; } v;

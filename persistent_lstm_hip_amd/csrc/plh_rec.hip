@@ -14,8 +14,10 @@
 //   * per step each wave computes its partial gate sums from h_{t-1} in LDS (32 MFMAs), the two
 //     K halves meet in LDS, and the two waves of a group split its 16 units x 16 rows (two units
 //     per lane), adding the bias and the precomputed input projection;
-//   * the slices exchange h_t every step through the tagged-word ring of plh_sliced.hip (same
-//     writer order, words and protocol); h_t also goes to the next layer's GEMM input.
+//   * the slices exchange h_t every step through a two-slot ring of tagged 64-bit words, with the
+//     protocol of plh_sliced.hip (readers re-poll words until their tags are current) but packed
+//     words: 4 fp16 and a 4-bit step tag each, and each workgroup polls only its 7 siblings;
+//     h_t also goes to the next layer's GEMM input, stored a step later from LDS.
 //
 // Reference behaviour restated (mantuoluozk/persistent_lstm_hip): the generic path's per-layer
 // input projection followed by a persistent recurrence (persistent_lstm_hip.cu:2923-3181), gate

@@ -71,7 +71,9 @@ int plh_pack_regressor(int input_size, int hidden_size, int num_layers, int outp
                        const void* const* b_hh, const void* lin_w, const void* lin_b,
                        void* packed_dev, int64_t packed_bytes, void* stream);
 
-/* Bytes of device workspace plh_forward needs for (geometry, batch, seq_len). */
+/* Bytes of device workspace plh_forward needs for (geometry, batch, seq_len).  At padded H 512 it
+ * depends on the path the launch plan picks for that batch and length (the layer-sequential one
+ * holds a layer's input projection for every step: about 3 MB per step at 512 rows). */
 int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int output_size, int batch,
                             int seq_len);
 
@@ -88,7 +90,9 @@ int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int
  *             probe_h / probe_c device fp32 [n_probe, L, batch, H] receive every layer's state
  *             after that many steps (h as rounded to fp16, c in fp32).  n_probe = 0: no probes.
  *   workspace device memory of at least plh_workspace_bytes(...) bytes, 256-byte aligned.
- * Any output pointer may be NULL.  Asynchronous on `stream`.
+ * Any output pointer may be NULL.  Asynchronous on `stream`.  At padded H 512, batches that need
+ * several wavefront launches run layer by layer instead (a rocBLAS fp16 GEMM per layer for the
+ * input projection, then a W_hh-only persistent kernel), when the launch plan models that as faster.
  * Replaces persistent_lstm4_forward_interleaved (bindings.cpp:157, persistent_lstm_hip.cu:2126-2254)
  * and persistent_lstm_regressor_forward_generic_projected (bindings.cpp:163,
  * persistent_lstm_hip.cu:2923-3181), whose signatures return only the [batch, O] head output;
@@ -107,7 +111,8 @@ int plh_status(const void* workspace, uint32_t* status, void* stream);
 /*
  * Optional timing of the persistent kernel alone (for benchmarks and profilers of the caller).
  * plh_kernel_timing(n) with n > 0 arms n pairs of HIP events for the calling thread: each later
- * plh_forward on this thread records one pair around its persistent launch(es), until the n pairs
+ * plh_forward on this thread records one pair around its persistent launch(es) (on the
+ * layer-sequential H512 path: around all its projection GEMMs and launches), until the n pairs
  * are used.  plh_kernel_timing(0) disarms.  plh_kernel_timing_read synchronises on the recorded
  * events and returns the summed elapsed milliseconds and the number of timed forwards.
  * No counterpart in the reference (it only timed whole forwards from Python, LSTM-hip.py:80-91).

@@ -102,11 +102,12 @@ Plan plan_path(const plh::Geometry& g, int batch, bool need_device, hipError_t* 
   return make_plan(g, batch, cap8, cap16);
 }
 
-// Where both paths exist (HP = 512), the one with the smaller modelled time on an MI355X: the
-// wavefront path runs T + L - 1 steps of about 3.7 us per launch of cap / (16 L) tiles (all
-// layers at once), the layer-sequential path L x T steps of about 4.7 us per launch of up to 512
-// rows plus about 1.1 us of projection GEMM per step and layer.  Small batches fit one wavefront
-// launch and keep it; large ones need several, and the layer-sequential path wins.  Its workspace
+// Where both paths exist (HP = 512), the one with the smaller modelled time on an MI355X
+// (measured): the wavefront path runs T + L - 1 steps of about 3.78 us per launch of cap / (16 L)
+// tiles (all layers at once), the layer-sequential path L x T steps of about 3.57 us per launch of
+// up to 512 rows plus about 1 us of projection GEMM per step and layer at 512 rows (proportionally
+// less for fewer rows).  Small batches fit one or a few wavefront launches and keep them; from
+// about 4.3 launches' worth of rows on, the layer-sequential path wins.  Its workspace
 // holds a layer's projections for every step (~3 MB per step at 512 rows); sequences that would
 // need more than kMaxSeqWorkspace stay on the wavefront path (~0.2 MB per step).
 constexpr size_t kMaxSeqWorkspace = (size_t)24 << 30;
@@ -119,8 +120,10 @@ Plan plan_for(const plh::Geometry& g, int batch, int seq_len, bool need_device, 
   q.rec = true;
   if (plh::workspace_layout(gr, seq_len, q.chunk_rows, q.tile_rows).total > kMaxSeqWorkspace) return p;
   const long long B = std::max(batch, 1), T = std::max(seq_len, 1);
-  const long long t_wave = 37 * ((B + p.chunk_rows - 1) / p.chunk_rows) * (T + g.L - 1);
-  const long long t_seq = 58 * g.L * ((B + q.chunk_rows - 1) / q.chunk_rows) * T;
+  const long long n_wave = (B + p.chunk_rows - 1) / p.chunk_rows, n_seq = (B + q.chunk_rows - 1) / q.chunk_rows;
+  const long long rows = (B + n_seq - 1) / n_seq;  // per layer-sequential launch
+  const long long t_wave = 378 * n_wave * (T + g.L - 1);  // units of 10 ns
+  const long long t_seq = n_seq * g.L * T * (357 + 100 * rows / 512);
   return t_seq < t_wave ? q : p;
 }
 

@@ -90,9 +90,13 @@ int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int
  *             probe_h / probe_c device fp32 [n_probe, L, batch, H] receive every layer's state
  *             after that many steps (h as rounded to fp16, c in fp32).  n_probe = 0: no probes.
  *   workspace device memory of at least plh_workspace_bytes(...) bytes, 256-byte aligned.
- * Any output pointer may be NULL.  Asynchronous on `stream`.  At padded H 512, batches that need
- * several wavefront launches run layer by layer instead (a rocBLAS fp16 GEMM per layer for the
- * input projection, then a W_hh-only persistent kernel), when the launch plan models that as faster.
+ * Any output pointer may be NULL.  Asynchronous on `stream`.  At padded H 512, a batch that needs
+ * more wavefront launches than there are layers runs layer by layer instead: per layer the input
+ * projection of every step as one fp16 MFMA GEMM (plh_input_projection's kernel; for layer 0 with
+ * input_size <= 32 inside the recurrent kernel), then a W_hh-only persistent kernel.  That path
+ * rounds x_t W_ih^T to fp16 before the recurrent sum, as the reference's generic path does
+ * (persistent_lstm_hip.cu:2988-2994); the all-layers path keeps it in fp32, so at padded H 512 the
+ * batch size decides which of the two roundings a row gets (both are within the tolerance).
  * Replaces persistent_lstm4_forward_interleaved (bindings.cpp:157, persistent_lstm_hip.cu:2126-2254)
  * and persistent_lstm_regressor_forward_generic_projected (bindings.cpp:163,
  * persistent_lstm_hip.cu:2923-3181), whose signatures return only the [batch, O] head output;
@@ -103,6 +107,25 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
                 const void* c0, void* out, void* out_seq, void* h_n, void* c_n,
                 const int32_t* probe_steps, int n_probe, float* probe_h, float* probe_c, void* workspace,
                 int64_t workspace_bytes, void* stream);
+
+/*
+ * Time-parallel input projection: out[m][n] = sum_{j < k} x[m][j] * w[n][j] for m < rows, n < cols,
+ * fp16 operands and result, fp32 accumulation (MFMA), e.g. one layer's x_t W_ih^T for all T steps
+ * of a batch at once (rows = T * batch).
+ *   w   device fp16 [cols][k] row-major
+ *   blocked = 0: x device fp16 [rows][ldx], out [rows][ldo], row-major
+ *   blocked = 1: x and out fragment-blocked, [rows / 16][ld / 32][64][8] halfs: element (r, c) at
+ *            (((r / 16) * (ld / 32) + c / 32) * 64 + ((c % 32) / 8) * 16 + r % 16) * 8 + c % 8, so that
+ *            every 16 rows x 32 columns are one contiguous 1 KB block (the layout of the
+ *            layer-sequential path's layer inputs and projections; the faster form)
+ * Requires k % 128 == 0, k <= 512, cols % 128 == 0, ldx >= k and ldo >= cols multiples of 8
+ * (blocked: of 32, and rows % 16 == 0), 16-byte aligned pointers (PLH_ERR_INVALID otherwise;
+ * zero-pad K to meet them).  Asynchronous on `stream`.
+ * Replaces the reference's torch::matmul input projections of fp16 tensors (the generic path's
+ * x.matmul(W_ih^T), persistent_lstm_hip.cu:2988-2994; the projected path's, :2329-2379).
+ */
+int plh_input_projection(const void* x, int64_t ldx, const void* w, int k, void* out, int64_t ldo, int64_t rows,
+                         int cols, int blocked, void* stream);
 
 /* Synchronise `stream` and read the status word the last plh_forward left in `workspace`
  * (0 = success, else PLH_STATUS_* bits).  Returns PLH_OK or PLH_ERR_HIP. */

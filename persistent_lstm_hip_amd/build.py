@@ -18,8 +18,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpersistent_lstm_hip.so")
 BENCH_PATH = os.path.join(LIB_DIR, "plh_bench")
-SOURCES = ["plh_wavefront.hip", "plh_sliced.hip", "plh_rec.hip", "plh_pack.hip", "plh_launch.hip", "plh_probe.hip",
-           "plh_capi.hip"]
+SOURCES = ["plh_wavefront.hip", "plh_sliced.hip", "plh_rec.hip", "plh_gemm.hip", "plh_pack.hip", "plh_launch.hip",
+           "plh_probe.hip", "plh_capi.hip"]
 HEADERS = ["plh_internal.h", os.path.join("..", "..", "include", "persistent_lstm_hip.h")]
 
 ARCH = "gfx950"
@@ -34,9 +34,8 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-command-line-argument",
 ]
-ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
-# rocBLAS computes the layer-sequential path's input projection (one GEMM per layer).
-LINK_FLAGS = ["-L" + ROCM_LIB, "-lrocblas", "-Wl,-rpath," + ROCM_LIB]
+# Only the HIP runtime (hipcc links it); every kernel is in csrc/, no vendor math library.
+LINK_FLAGS: list = []
 
 
 def hipcc() -> str:

@@ -5,7 +5,6 @@
 // std::runtime_error): here they become PLH_ERR_INVALID / PLH_ERR_HIP plus a message.  Unlike the
 // reference there is no silent fallback: a geometry the kernels do not implement is an error.
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <climits>
@@ -102,14 +101,12 @@ Plan plan_path(const plh::Geometry& g, int batch, bool need_device, hipError_t* 
   return make_plan(g, batch, cap8, cap16);
 }
 
-// Where both paths exist (HP = 512), the one with the smaller modelled time on an MI355X
-// (measured): the wavefront path runs T + L - 1 steps of about 3.78 us per launch of cap / (16 L)
-// tiles (all layers at once), the layer-sequential path L x T steps of about 3.57 us per launch of
-// up to 512 rows plus about 1 us of projection GEMM per step and layer at 512 rows (proportionally
-// less for fewer rows).  Small batches fit one or a few wavefront launches and keep them; from
-// about 4.3 launches' worth of rows on, the layer-sequential path wins.  Its workspace
-// holds a layer's projections for every step (~3 MB per step at 512 rows); sequences that would
-// need more than kMaxSeqWorkspace stay on the wavefront path (~0.2 MB per step).
+// Where both paths exist (HP = 512), a fixed rule on step counts picks one: the wavefront path runs
+// T + L - 1 steps per launch of all L layers, the layer-sequential path L x T steps per launch of up
+// to 512 rows of one layer (plus one projection GEMM per layer after the first).  The
+// layer-sequential path is used when the batch needs more wavefront launches than there are layers
+// (so it does fewer launches of recurrent steps), and only while its workspace - a layer's
+// projections for every step, ~4 MB per step at 512 rows - stays within kMaxSeqWorkspace.
 constexpr size_t kMaxSeqWorkspace = (size_t)24 << 30;
 Plan plan_for(const plh::Geometry& g, int batch, int seq_len, bool need_device, hipError_t* err) {
   const Plan p = plan_path(g, batch, need_device, err);
@@ -119,12 +116,8 @@ Plan plan_for(const plh::Geometry& g, int batch, int seq_len, bool need_device, 
   if (*err != hipSuccess) return p;
   q.rec = true;
   if (plh::workspace_layout(gr, seq_len, q.chunk_rows, q.tile_rows).total > kMaxSeqWorkspace) return p;
-  const long long B = std::max(batch, 1), T = std::max(seq_len, 1);
-  const long long n_wave = (B + p.chunk_rows - 1) / p.chunk_rows, n_seq = (B + q.chunk_rows - 1) / q.chunk_rows;
-  const long long rows = (B + n_seq - 1) / n_seq;  // per layer-sequential launch
-  const long long t_wave = 378 * n_wave * (T + g.L - 1);  // units of 10 ns
-  const long long t_seq = n_seq * g.L * T * (357 + 100 * rows / 512);
-  return t_seq < t_wave ? q : p;
+  const long long n_wave = (std::max(batch, 1) + (long long)p.chunk_rows - 1) / p.chunk_rows;
+  return n_wave > g.L ? q : p;
 }
 
 bool geometry(int I, int H, int L, int O, plh::Geometry* g) {
@@ -142,70 +135,49 @@ int geometry_code(int I, int H, int L, int O) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Armed timing events of the calling thread (plh_kernel_timing).
+// Armed timing events of the calling thread (plh_kernel_timing).  Held through a pointer that is
+// never deleted: a thread_local object's destructor would run at thread or process exit, possibly
+// after the HIP runtime has been torn down, so the library makes no HIP call from a destructor.
+// Events are released only by plh_kernel_timing() itself (re-arming or disarming).
 struct KernelTiming {
   std::vector<hipEvent_t> ev;  // begin/end pairs
   int used = 0;                // pairs recorded
-  ~KernelTiming() { release(); }
   void release() {
     for (hipEvent_t e : ev) (void)hipEventDestroy(e);
     ev.clear();
     used = 0;
   }
 };
-thread_local KernelTiming g_timing;
+thread_local KernelTiming* g_timing_ptr = nullptr;
+KernelTiming& timing() {
+  if (!g_timing_ptr) g_timing_ptr = new KernelTiming();
+  return *g_timing_ptr;
+}
 
 // Bound on inter-workgroup waits of this thread's forwards (plh_set_wait_limit_us).
 constexpr int64_t kDefaultWaitUs = 2000000;
 thread_local int64_t g_wait_us = kDefaultWaitUs;
 
-// rocBLAS handle of the calling thread on each device (the layer-sequential input projection).  A
-// handle is not shared between threads (its stream is per call); handles live until the process ends.
-rocblas_handle blas_handle(int dev, rocblas_status* st) {
-  thread_local std::unordered_map<int, rocblas_handle>* handles = new std::unordered_map<int, rocblas_handle>();
-  auto it = handles->find(dev);
-  if (it != handles->end()) {
-    *st = rocblas_status_success;
-    return it->second;
-  }
-  rocblas_handle h = nullptr;
-  *st = rocblas_create_handle(&h);
-  if (*st != rocblas_status_success) return nullptr;
-  (*handles)[dev] = h;
-  return h;
-}
+// Compute units of the current device (the persistent projection GEMM's grid), queried once per
+// device.
+std::mutex g_cus_mu;
+std::unordered_map<int, int> g_cus;
 
-// gates[t][r][c] = sum_k in[t][r][k] w_ih[c][k] for the T x rows_pad rows of a launch and the 4 HP
-// lane-ordered columns (fp16 operands and result, fp32 accumulation: the reference's torch::matmul
-// of fp16 tensors, persistent_lstm_hip.cu:2988-2991), split so that no call exceeds 32-bit element
-// counts.
-int input_projection(const plh::Geometry& g, const _Float16* w_ih, int K, const _Float16* in, _Float16* gates,
-                     int T, int rows_pad, hipStream_t s) {
-  if (T == 0 || rows_pad == 0) return PLH_OK;
+int device_cus(hipError_t* err) {
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail_hip(e, "device query");
-  rocblas_status st;
-  rocblas_handle h = blas_handle(dev, &st);
-  if (st == rocblas_status_success) st = rocblas_set_stream(h, s);
-  if (st != rocblas_status_success)
-    return fail(PLH_ERR_HIP, std::string("rocBLAS handle: ") + rocblas_status_to_string(st));
-  const int m = 4 * g.HP;
-  const int steps = std::max(1, (int)std::min<long long>(T, INT_MAX / ((long long)m * rows_pad)));
-  const float alpha = 1.0f, beta = 0.0f;
-  for (int t0 = 0; t0 < T; t0 += steps) {
-    const int n = std::min(steps, T - t0) * rows_pad;
-    const _Float16* b = in + (size_t)t0 * rows_pad * g.HP;
-    _Float16* c = gates + (size_t)t0 * rows_pad * m;
-    // Column-major view: C (m x n, ldc m) = A^T B with A = w_ih as stored (K x m, lda K) and
-    // B = in (K x n, ldb HP).
-    st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, m, n, K, &alpha, w_ih,
-                         rocblas_datatype_f16_r, K, b, rocblas_datatype_f16_r, g.HP, &beta, c, rocblas_datatype_f16_r,
-                         m, c, rocblas_datatype_f16_r, m, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success)
-      return fail(PLH_ERR_HIP, std::string("rocblas_gemm_ex (input projection): ") + rocblas_status_to_string(st));
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return 0;
+  {
+    std::lock_guard<std::mutex> lk(g_cus_mu);
+    auto it = g_cus.find(dev);
+    if (it != g_cus.end()) return it->second;
   }
-  return PLH_OK;
+  int cus = 0;
+  *err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (*err != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lk(g_cus_mu);
+  g_cus[dev] = cus;
+  return cus;
 }
 
 }  // namespace
@@ -249,13 +221,19 @@ int plh_pack_regressor(int input_size, int hidden_size, int num_layers, int outp
                                           (_Float16*)(base + p.wpack), s);
     if (e != hipSuccess) return fail_hip(e, "pack_layer launch");
     if (g.rec_ok) {
-      // The layer-sequential path's operands: W_hh fragments, W_ih as the projection GEMM's A.
+      // The layer-sequential path's operands: W_hh fragments; W_ih as the projection GEMM's W operand,
+      // or for layer 0 with I <= 32 as the recurrent kernel's MFMA fragments.
       e = plh::launch_pack_rec_layer(g, l, (const _Float16*)w_hh[l], (_Float16*)(base + p.wrec), s);
       if (e != hipSuccess) return fail_hip(e, "pack_rec_layer launch");
-      const int K = l == 0 ? g.I : g.H;
-      e = plh::launch_pack_rec_wih(g, (const _Float16*)w_ih[l], K, (_Float16*)(base + wih_off), s);
-      if (e != hipSuccess) return fail_hip(e, "pack_rec_wih launch");
-      wih_off += (size_t)4 * g.HP * K * sizeof(_Float16);
+      if (l == 0 && g.rec_x0) {
+        e = plh::launch_pack_rec_wx0(g, (const _Float16*)w_ih[0], (_Float16*)(base + p.wx0), s);
+        if (e != hipSuccess) return fail_hip(e, "pack_rec_wx0 launch");
+      } else {
+        const int K = l == 0 ? g.I : g.H, Kp = l == 0 ? g.kp0 : g.kp;
+        e = plh::launch_pack_rec_wih(g, (const _Float16*)w_ih[l], K, Kp, (_Float16*)(base + wih_off), s);
+        if (e != hipSuccess) return fail_hip(e, "pack_rec_wih launch");
+        wih_off += (size_t)4 * g.HP * Kp * sizeof(_Float16);
+      }
     }
     e = plh::launch_pack_bias(g, l, (const _Float16*)b_ih[l], b_hh ? (const _Float16*)b_hh[l] : nullptr,
                               (float*)(base + p.bias), s);
@@ -354,7 +332,10 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   a.g_in0 = g.g_in0;
   a.wait_ticks = (uint64_t)g_wait_us * 100u;  // s_memrealtime: 100 MHz
 
-  const bool timed = g_timing.used * 2 < (int)g_timing.ev.size();
+  KernelTiming& tm = timing();
+  const bool timed = tm.used * 2 < (int)tm.ev.size();
+  const int cus = g.rec ? device_cus(&err) : 0;
+  if (err != hipSuccess) return fail_hip(err, "device query");
   for (int row0 = 0; row0 < batch; row0 += chunk_rows) {
     const int rows = std::min(chunk_rows, batch - row0);
     a.row0 = row0;
@@ -366,83 +347,114 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     a.rows_pad = a.ntile * plan.tile_rows;
     a.xcd_map = ((g.slices > 1 && !g.rec) ? (g.L * a.ntile / a.wg_tiles) % 8 : a.ntile % 8) == 0 ? 1 : 0;
     if (g.rec) {
-      // Layer by layer: x of this chunk into xs slot 0; per layer the input projection of every
-      // step (one GEMM), the exchange ring cleared (tags restart at 1), and the recurrent kernel,
-      // whose h sequence goes to the other xs slot as the next layer's input.
+      // Layer by layer.  Layer 0: with I <= 32 its input projection runs inside the recurrent kernel
+      // from x packed by the prologue; otherwise x goes to xs slot 0 for the projection GEMM.  Every
+      // later layer: the projection GEMM of every step (plh_gemm.hip) over the previous layer's h
+      // sequence, then the recurrent kernel, whose h sequence goes to the other xs slot.  The
+      // exchange ring is cleared before each layer's launch (tags restart at 1).
       _Float16* xs[2] = {(_Float16*)(ws + w.xs),
                          (_Float16*)(ws + w.xs) + (size_t)seq_len * chunk_rows * g.HP};
-      if (row0 == 0) {
-        err = plh::launch_zero_u32(status, 1, s);
-        if (err != hipSuccess) return fail_hip(err, "status reset");
-        if (timed) {
-          err = hipEventRecord(g_timing.ev[2 * g_timing.used], s);
-          if (err != hipSuccess) return fail_hip(err, "timing event");
-        }
+      _Float16* gates = (_Float16*)(ws + w.gates);
+      err = plh::launch_forward_prologue(g, a, row0 == 0 ? status : nullptr, g.rec_x0 ? 4 : 0, w.xring_words, s);
+      if (err != hipSuccess) return fail_hip(err, "forward prologue");
+      if (timed && row0 == 0) {
+        err = hipEventRecord(tm.ev[2 * tm.used], s);
+        if (err != hipSuccess) return fail_hip(err, "timing event");
       }
-      err = plh::launch_rec_input(g, a, xs[0], s);
-      if (err != hipSuccess) return fail_hip(err, "input transpose");
+      if (!g.rec_x0) {
+        err = plh::launch_rec_input(g, a, xs[0], s);
+        if (err != hipSuccess) return fail_hip(err, "input transpose");
+      }
       const _Float16* wih = (const _Float16*)(pk + p.wih);
-      a.gates = (const _Float16*)(ws + w.gates);
+      a.gates = gates;
       for (int l = 0; l < g.L; ++l) {
-        const int K = l == 0 ? g.I : g.H;
-        const int rc = input_projection(g, wih, K, xs[l & 1], (_Float16*)(ws + w.gates), seq_len, a.rows_pad, s);
-        if (rc != PLH_OK) return rc;
-        wih += (size_t)4 * g.HP * K;
-        err = plh::launch_zero_u32((uint32_t*)a.xring, w.xring_words * 2, s);
-        if (err != hipSuccess) return fail_hip(err, "exchange ring reset");
+        const bool x0 = l == 0 && g.rec_x0;
+        if (!x0) {
+          const int Kp = l == 0 ? g.kp0 : g.kp;
+          err = plh::launch_proj_gemm(xs[l & 1], g.HP, wih, Kp, gates, 4 * g.HP, (long long)seq_len * a.rows_pad,
+                                      4 * g.HP, true, cus, s);
+          if (err != hipSuccess) return fail_hip(err, "input projection GEMM launch");
+          wih += (size_t)4 * g.HP * Kp;
+        }
+        if (l > 0) {
+          err = plh::launch_zero_u32((uint32_t*)a.xring, w.xring_words * 2, s);
+          if (err != hipSuccess) return fail_hip(err, "exchange ring reset");
+        }
         a.layer = l;
         a.hout = l + 1 < g.L ? xs[(l + 1) & 1] : nullptr;
+        a.wx0 = x0 ? (const _Float16*)(pk + p.wx0) : nullptr;
         err = plh::launch_recurrent(g, a, s);
         if (err != hipSuccess) return fail_hip(err, "persistent LSTM launch");
       }
+      a.wx0 = nullptr;
       continue;
     }
     // x of this launch's rows into xp; status (first launch), counters and, when sliced, the
     // exchange ring (tags restart at 1) cleared: one launch ahead of the persistent one
-    err = plh::launch_forward_prologue(g, a, row0 == 0 ? status : nullptr, s);
+    err = plh::launch_forward_prologue(g, a, row0 == 0 ? status : nullptr, g.g_in0, w.xring_words, s);
     if (err != hipSuccess) return fail_hip(err, "forward prologue");
     if (timed && row0 == 0) {
-      err = hipEventRecord(g_timing.ev[2 * g_timing.used], s);
+      err = hipEventRecord(tm.ev[2 * tm.used], s);
       if (err != hipSuccess) return fail_hip(err, "timing event");
     }
     err = plh::launch_recurrent(g, a, s);
     if (err != hipSuccess) return fail_hip(err, "persistent LSTM launch");
   }
   if (timed) {
-    err = hipEventRecord(g_timing.ev[2 * g_timing.used + 1], s);
+    err = hipEventRecord(tm.ev[2 * tm.used + 1], s);
     if (err != hipSuccess) return fail_hip(err, "timing event");
-    ++g_timing.used;
+    ++tm.used;
   }
   return PLH_OK;
 }
 
 int plh_kernel_timing(int max_forwards) {
-  g_timing.release();
+  KernelTiming& tm = timing();
+  tm.release();
   if (max_forwards < 0) return fail(PLH_ERR_INVALID, "max_forwards must be non-negative");
   for (int i = 0; i < 2 * max_forwards; ++i) {
     hipEvent_t e;
     hipError_t err = hipEventCreate(&e);
     if (err != hipSuccess) {
-      g_timing.release();
+      tm.release();
       return fail_hip(err, "timing event creation");
     }
-    g_timing.ev.push_back(e);
+    tm.ev.push_back(e);
   }
   return PLH_OK;
 }
 
 int plh_kernel_timing_read(double* total_ms, int* forwards) {
   if (!total_ms || !forwards) return fail(PLH_ERR_INVALID, "total_ms and forwards are required");
+  KernelTiming& tm = timing();
   double sum = 0.0;
-  for (int i = 0; i < g_timing.used; ++i) {
+  for (int i = 0; i < tm.used; ++i) {
     float ms = 0.0f;
-    hipError_t err = hipEventSynchronize(g_timing.ev[2 * i + 1]);
-    if (err == hipSuccess) err = hipEventElapsedTime(&ms, g_timing.ev[2 * i], g_timing.ev[2 * i + 1]);
+    hipError_t err = hipEventSynchronize(tm.ev[2 * i + 1]);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, tm.ev[2 * i], tm.ev[2 * i + 1]);
     if (err != hipSuccess) return fail_hip(err, "timing read");
     sum += ms;
   }
   *total_ms = sum;
-  *forwards = g_timing.used;
+  *forwards = tm.used;
+  return PLH_OK;
+}
+
+int plh_input_projection(const void* x, int64_t ldx, const void* w, int k, void* out, int64_t ldo, int64_t rows,
+                         int cols, int blocked, void* stream) {
+  if (blocked != 0 && blocked != 1) return fail(PLH_ERR_INVALID, "blocked must be 0 or 1");
+  if (!plh::gemm_shape_ok(rows, cols, k, ldx, ldo, blocked != 0))
+    return fail(PLH_ERR_INVALID, "plh_input_projection needs rows >= 0, cols % 128 == 0, k % 128 == 0, k <= 512, "
+                                 "ldx >= k and ldo >= cols (multiples of 8; blocked: of 32, rows % 16 == 0)");
+  if (rows > 0 && (!x || !w || !out)) return fail(PLH_ERR_INVALID, "x, w and out are required");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16))
+    return fail(PLH_ERR_INVALID, "x, w and out must be 16-byte aligned");
+  hipError_t err = hipSuccess;
+  const int cus = device_cus(&err);
+  if (err != hipSuccess) return fail_hip(err, "device query");
+  err = plh::launch_proj_gemm((const _Float16*)x, ldx, (const _Float16*)w, k, (_Float16*)out, ldo, rows, cols,
+                              blocked != 0, cus, (hipStream_t)stream);
+  if (err != hipSuccess) return fail_hip(err, "input projection GEMM launch");
   return PLH_OK;
 }
 

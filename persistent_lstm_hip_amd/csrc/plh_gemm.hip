@@ -1,0 +1,202 @@
+// plh_gemm.hip -- the time-parallel input projection of the layer-sequential path on CDNA4 (gfx950):
+//
+//     C[m][n] = sum_k X[m][k] * W[n][k]        fp16 operands, fp32 accumulation, fp16 result
+//
+// X is a layer's input sequence for every (step, row) of a launch ([T * rows][ldx], K-contiguous),
+// W is that layer's W_ih ([N = 4 HP][K], K-contiguous, rows in the recurrent kernel's lane order),
+// C the gate pre-activations the recurrent kernel reads two steps ahead.  It restates the
+// reference's per-layer torch::matmul of fp16 tensors (persistent_lstm_hip.cu:2988-2994, fp16
+// result), written as a hand-written MFMA kernel instead of a library GEMM.
+//
+// Design (K <= 512, so a 128-column slice of W is at most 128 KB):
+//   * weight-stationary: each workgroup owns one 128-column slice of W, loaded once into LDS in MFMA
+//     fragment order, and walks the 512-row m-tiles of its m-group; its 8 waves (two per SIMD) each
+//     compute a 64 (m) x 128 (n) sub-tile with v_mfma_f32_16x16x32_f16 (4 x 8 accumulator tiles,
+//     128 fp32 per lane), W as the MFMA's A operand and X as its B operand;
+//   * X goes from global memory straight into the B-fragment registers (a lane's 8 consecutive k
+//     of one row are one 16-byte load), through a ring of 4 k-steps of 32: the loads of step s + 3
+//     are issued before the MFMAs of step s, across tile boundaries, so a load has three steps
+//     (~3000 cycles with the other wave of the SIMD) to arrive; the waves never synchronise after
+//     the weight load;
+//   * W's rows are placed in the fragment blocks of an n-tile pair (2p, 2p + 1) so that lane l of
+//     tile 2p + h holds n = 32 p + 8 (l / 16) + 4 h + 0..3: the lane's two accumulators are 8
+//     consecutive n, stored as one 16-byte write (row m = l % 16);
+//   * XCD-aware placement: workgroups are dispatched round-robin over the 8 XCDs (workgroup b on
+//     XCD b % 8), and the n-slices of one m-group share an XCD, so each m-tile of X is read from
+//     HBM about once into that XCD's L2 and then from L2 by the other slices;
+//   * two layouts of X and C: row-major ([M][ldx], [M][ldc]), or fragment-blocked: X as
+//     [M / 16][ldx / 32][64 lanes][8] (block (mb, kc) holds rows 16 mb + l % 16, k = 32 kc + 8 (l / 16)
+//     + 0..7 in lane l) and C as [M / 16][ldc / 32][64][8] (n = 32 g + 8 (l / 16) + 0..7).  A lane's
+//     16 bytes then sit at lane * 16 of a 1 KB block, so every load and store instruction of a wave
+//     moves 1 KB of whole cache lines (row-major: 16 rows x 64 B).  The layer-sequential path keeps
+//     its layer inputs and projections blocked (the recurrent kernel writes and reads them so).
+// Requirements (checked by the host): K % 128 == 0, K <= 512, N % 128 == 0, ldx and ldc multiples
+// of 8 (blocked: of 32, and M % 16 == 0), 16-byte aligned pointers.  Rows m >= M are not stored
+// (their loads are clamped to row M - 1).
+#include <algorithm>
+
+#include "plh_device.h"
+
+namespace plh {
+namespace {
+
+#ifndef PLH_GEMM_WAVES
+#define PLH_GEMM_WAVES 8
+#endif
+#ifndef PLH_GEMM_RING
+#define PLH_GEMM_RING 4
+#endif
+constexpr int kGemmWaves = PLH_GEMM_WAVES;            // waves per workgroup
+constexpr int kGemmWM = 32 / kGemmWaves;              // 16-row m-tiles per wave
+constexpr int kGemmBM = kGemmWaves * kGemmWM * 16;    // rows per m-tile of a workgroup (512)
+constexpr int kGemmBN = 128;                          // columns per workgroup (its W slice)
+constexpr int kGemmMaxK = 512;                        // W slice of 128 x 512 fp16 = 128 KB of LDS
+constexpr int kRing = PLH_GEMM_RING;                  // X fragment ring depth (k-steps of 32)
+constexpr int kGemmKStep = 32 * kRing;                // K granule
+constexpr int kGemmThreads = kGemmWaves * 64;
+
+// Row (within the 128-column slice) of W held by row i of the A fragment of n-tile nt.
+__device__ __forceinline__ int gemm_w_row(int nt, int i) {
+  return 32 * (nt >> 1) + 8 * (i >> 2) + 4 * (nt & 1) + (i & 3);
+}
+
+template <bool BLK>
+__global__ void __launch_bounds__(kGemmThreads)
+proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* __restrict__ W, int K,
+                 _Float16* __restrict__ C, long long ldc, int M, int tiles_m, int n_slices, int m_groups) {
+  constexpr int WM = kGemmWM;
+  // W slice: [k-chunk of 32][n-tile 0..7][64 lanes] f16x8, k-chunk major.
+  __shared__ f16x8 wl[kGemmMaxK / 32 * 8 * 64];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // Workgroup -> (n-slice, m-group): the n-slices of an m-group share the XCD b % 8.
+  const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+  const int ns = idx % n_slices;
+  const int mg = (idx / n_slices) * 8 + xcd;
+  if (mg >= m_groups) return;
+  const int n0 = ns * kGemmBN;
+  const int KS = K / 32;  // k-steps per tile (a multiple of kRing)
+
+  // The W slice into LDS (once).
+  for (int e = threadIdx.x; e < KS * 8 * 64; e += kGemmThreads) {
+    const int l = e & 63, nt = (e >> 6) & 7, kc = e >> 9;
+    const int n = n0 + gemm_w_row(nt, l & 15);
+    wl[e] = *reinterpret_cast<const f16x8*>(W + (size_t)n * K + kc * 32 + (l >> 4) * 8);
+  }
+  __syncthreads();
+
+  // m-tiles of this m-group: mg, mg + m_groups, ...
+  int mt = mg;
+  if (mt >= tiles_m) return;
+  // X fragment a of k-step s of a tile: lane l reads row tile * BM + wave * 16 WM + 16 a + l % 16
+  // (clamped to M - 1), k = 32 s + 8 (l / 16) .. + 7.
+  const int lrow = wave * (16 * WM) + (lane & 15), lk = (lane >> 4) * 8;
+  // Blocked: the fragment (16-row block mb, k-chunk kc) is 64 f16x8 at (mb * ldx / 32 + kc) * 64; the
+  // returned pointer is that of kc = 0, and k-chunk kc is 64 f16x8 further per chunk.
+  auto xptr = [&](int tile, int a) -> const f16x8* {
+    if constexpr (BLK) {
+      int mb = (tile * kGemmBM + wave * (16 * WM)) / 16 + a;
+      mb = mb < M / 16 ? mb : M / 16 - 1;
+      return reinterpret_cast<const f16x8*>(X) + (size_t)mb * (ldx / 32) * 64 + lane;
+    }
+    int m = tile * kGemmBM + lrow + 16 * a;
+    m = m < M ? m : M - 1;
+    return reinterpret_cast<const f16x8*>(X + (size_t)m * ldx + lk);
+  };
+  constexpr int kStepVec = BLK ? 64 : 4;  // f16x8 from one k-chunk of 32 to the next
+  f16x8 xr[kRing][WM];
+  // Flat step f = (tile index within this workgroup) * KS + k-step; loads of step f go to ring slot
+  // f % kRing.  Prologue: steps 0 .. kRing - 2 of the first tile.
+#pragma unroll
+  for (int j = 0; j < kRing - 1; ++j)
+#pragma unroll
+    for (int a = 0; a < WM; ++a) xr[j][a] = xptr(mt, a)[j * kStepVec];
+
+  for (;;) {
+    const int nmt = mt + m_groups;
+    const int pmt = nmt < tiles_m ? nmt : mt;  // prefetch target past the last tile: reload this one
+    f32x4 acc[WM][8];
+#pragma unroll
+    for (int a = 0; a < WM; ++a)
+#pragma unroll
+      for (int b = 0; b < 8; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kq = 0; kq < KS; kq += kRing) {
+#pragma unroll
+      for (int j = 0; j < kRing; ++j) {
+        // Prefetch flat step + kRing - 1 into its slot: this tile's k-step kq + j + kRing - 1, or the
+        // next tile's first steps.
+        {
+          const int kn = kq + j + kRing - 1;
+          const bool nxt = kn >= KS;
+          const int t = nxt ? pmt : mt, kk = nxt ? kn - KS : kn;
+#pragma unroll
+          for (int a = 0; a < WM; ++a) xr[(j + kRing - 1) % kRing][a] = xptr(t, a)[kk * kStepVec];
+        }
+        const f16x8* wp = wl + (kq + j) * 8 * 64 + lane;
+        f16x8 wa[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) wa[b] = wp[b * 64];
+#pragma unroll
+        for (int a = 0; a < WM; ++a)
+#pragma unroll
+          for (int b = 0; b < 8; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[b], xr[j][a], acc[a][b], 0, 0, 0);
+      }
+    }
+    // Lane holds rows mt * BM + lrow + 16 a and, for n-tile pair p, columns n0 + 32 p + 8 (lane / 16)
+    // + 0..7.
+    const int mrow = mt * kGemmBM + lrow;
+    const int ncol = n0 + lk;
+#pragma unroll
+    for (int a = 0; a < WM; ++a) {
+      const int m = mrow + 16 * a;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        f16x8 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = (_Float16)acc[a][2 * p][j];
+          v[4 + j] = (_Float16)acc[a][2 * p + 1][j];
+        }
+        if (m < M) {
+          if constexpr (BLK)
+            reinterpret_cast<f16x8*>(C)[((size_t)(m >> 4) * (ldc / 32) + (n0 >> 5) + p) * 64 + lane] = v;
+          else
+            *reinterpret_cast<f16x8*>(C + (size_t)m * ldc + ncol + 32 * p) = v;
+        }
+      }
+    }
+    if (nmt >= tiles_m) break;
+    mt = nmt;
+  }
+}
+
+}  // namespace
+
+bool gemm_shape_ok(long long M, int N, int K, long long ldx, long long ldc, bool blocked) {
+  const int q = blocked ? 32 : 8;
+  return M >= 0 && N > 0 && K > 0 && N % kGemmBN == 0 && K % kGemmKStep == 0 && K <= kGemmMaxK && ldx >= K &&
+         ldc >= N && ldx % q == 0 && ldc % q == 0 && (!blocked || M % 16 == 0) && M <= (long long)INT32_MAX;
+}
+
+hipError_t launch_proj_gemm(const _Float16* X, long long ldx, const _Float16* W, int K, _Float16* C, long long ldc,
+                            long long M, int N, bool blocked, int cus, hipStream_t s) {
+  if (!gemm_shape_ok(M, N, K, ldx, ldc, blocked)) return hipErrorInvalidValue;
+  if (M == 0) return hipSuccess;
+  const int tiles_m = (int)((M + kGemmBM - 1) / kGemmBM), n_slices = N / kGemmBN;
+  // One workgroup per CU: n_slices per m-group, as many m-groups as fill the device (at most one per
+  // m-tile), placed so that an m-group's slices share an XCD.
+  const int m_groups = std::max(1, std::min(tiles_m, std::max(cus, 1) / n_slices));
+  const int grid = ((m_groups + 7) / 8) * 8 * n_slices;
+  if (blocked)
+    hipLaunchKernelGGL(proj_gemm_kernel<true>, dim3(grid), dim3(kGemmThreads), 0, s, X, ldx, W, K, C, ldc, (int)M,
+                       tiles_m, n_slices, m_groups);
+  else
+    hipLaunchKernelGGL(proj_gemm_kernel<false>, dim3(grid), dim3(kGemmThreads), 0, s, X, ldx, W, K, C, ldc, (int)M,
+                       tiles_m, n_slices, m_groups);
+  return hipGetLastError();
+}
+
+double proj_gemm_flops(long long M, int N, int K) { return 2.0 * (double)M * N * K; }
+
+}  // namespace plh

@@ -27,7 +27,11 @@ struct Geometry {
   int waves;   // waves per workgroup: HP / 16 (one per 16 hidden units) or 8 when sliced
   int kci;     // input-part K chunks of 32 for layers >= 1 (= HP / 32)
   int kc;      // K chunks of [W_ih | W_hh] per gate row (= 2 * kci)
-  int g_in0;   // 8-wide K groups of x per step that layer 0 reads (= ceil(I / 8) <= 4 * kci)
+  int g_in0;   // 8-wide K groups of x per step that layer 0 reads (= ceil(I / 8) <= 4 * kci); on the
+               // layer-sequential path with rec_x0, 4 (one zero-padded K chunk of 32)
+  int rec_x0;  // layer-sequential path: layer 0's input projection (I <= 32) is computed inside the
+               // recurrent kernel (one MFMA K chunk); otherwise by the projection GEMM like the others
+  int kp0, kp;  // K of the projection GEMM, padded to a multiple of 128: layer 0 (0 with rec_x0), layers >= 1
 };
 
 // Fills *g; returns false (with the reason) for geometries the kernels do not implement.
@@ -44,8 +48,11 @@ struct PackedLayout {
   size_t blin;   // f32 [O]
   size_t wrec;   // rec_ok: f16 W_hh fragments of the layer-sequential kernel, [L][8 slices][8 waves][8
                  // chunks][4 gates][64 lanes][8]
-  size_t wih;    // rec_ok: f16 W_ih of every layer as the projection GEMM's A operand, [4 HP][I], then
-                 // [4 HP][H] per layer: rows permuted to the kernel's lane order
+  size_t wih;    // rec_ok: f16 W_ih of every layer the projection GEMM computes, as its W operand:
+                 // [4 HP][kp0] (layer 0, unless rec_x0), then [4 HP][kp] per layer >= 1; rows permuted to the
+                 // recurrent kernel's lane order, K zero-padded
+  size_t wx0;    // rec_ok with rec_x0: f16 MFMA A fragments of W_ih of layer 0 for the recurrent kernel,
+                 // [8 slices][8 waves][2 gates][64 lanes][8] (wave w: unit group w % 4, gates 2 (w / 4) + 0..1)
   size_t total;
 };
 PackedLayout packed_layout(const Geometry& g);
@@ -60,9 +67,13 @@ PackedLayout packed_layout(const Geometry& g);
 //   xring    u64 [L][ntile][2][HP * 8]             sliced geometries only: per-step exchange of h
 //                                                  among the slices of a (layer, tile), tagged words
 // Layer-sequential geometries (one layer per launch) use instead of xp and hseq:
-//   gates    f16 [T][rows][4 HP]                   one layer's input projection x_t W_ih^T, columns
+//   gates    f16 [T * rows][4 HP] fragment-blocked one layer's input projection x_t W_ih^T, columns
 //                                                  in the recurrent kernel's lane order
-//   xs       f16 [2][T][rows][HP]                  layer inputs/outputs, alternating (x in slot 0)
+//   xs       f16 [2][T * rows][HP] fragment-blocked layer inputs/outputs, alternating (x in slot 0
+//                                                  when layer 0's projection is a GEMM)
+// (fragment-blocked: see blocked_index; one 1 KB block per 16 rows x 32 columns)
+//   xp       f16x8 [ntile][T][4][16]               with rec_x0: x in B-fragment order, K zero-padded
+//                                                  to 32 (layer 0's in-kernel projection)
 // and an xring of one layer.
 struct WorkspaceLayout {
   size_t status, counters, xp, hseq, xring, gates, xs, total;
@@ -104,8 +115,9 @@ struct ForwardArgs {
   int wg_tiles;                 // sliced kernels: 16-row tiles per workgroup (1 or 2); ntile is a multiple
   // layer-sequential kernel (one layer per launch):
   int layer;                    // the layer this launch runs
-  const _Float16* gates;        // [T][rows_pad][4 HP] input projection of that layer (no bias), lane order
-  _Float16* hout;               // [T][rows_pad][HP] its h sequence, the next layer's input (null: last layer)
+  const _Float16* gates;        // [T * rows_pad][4 HP] blocked: input projection of that layer (no bias), lane order
+  _Float16* hout;               // [T * rows_pad][HP] blocked: its h sequence, the next layer's input (null: last layer)
+  const _Float16* wx0;          // rec_x0, layer 0: W_ih fragments of the in-kernel projection (x from xp)
 };
 
 hipError_t launch_pack_layer(const Geometry& g, int layer, const _Float16* w_ih, const _Float16* w_hh,
@@ -114,9 +126,11 @@ hipError_t launch_pack_bias(const Geometry& g, int layer, const _Float16* b_ih, 
                             float* bias, hipStream_t s);
 hipError_t launch_pack_linear(const Geometry& g, const _Float16* w, const _Float16* b, float* wlin,
                               float* blin, hipStream_t s);
-// One launch before each persistent launch: packs this launch's x into xp and clears the status
-// word (if `status`), the counters and (sliced) the exchange ring.
-hipError_t launch_forward_prologue(const Geometry& g, const ForwardArgs& a, uint32_t* status, hipStream_t s);
+// One launch before each persistent launch: packs this launch's x into xp (g0 8-wide K groups per
+// row and step, zero past I) and clears the status word (if `status`), the counters and ring_words
+// u64 words of the exchange ring.
+hipError_t launch_forward_prologue(const Geometry& g, const ForwardArgs& a, uint32_t* status, int g0,
+                                   size_t ring_words, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t s);
 hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, int cols, hipStream_t s);
 
@@ -131,12 +145,31 @@ int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err);
 hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s);
 
 // Layer-sequential path (plh_rec.hip): W_hh fragments of one layer, x of a launch's rows into
-// xs slot 0 ([T][rows_pad][HP], zero past the launch's rows), and the recurrent kernel of a.layer.
+// xs slot 0 (blocked [T * rows_pad][HP], zero past the launch's rows and past I up to kp0), and the
+// recurrent kernel of a.layer (x0: with layer 0's in-kernel input projection).
 hipError_t launch_pack_rec_layer(const Geometry& g, int layer, const _Float16* w_hh, _Float16* wpack, hipStream_t s);
 hipError_t launch_rec_input(const Geometry& g, const ForwardArgs& a, _Float16* xs0, hipStream_t s);
-// W_ih ([4H][K]) of one layer as the projection GEMM's A operand ([4 HP][K], lane-ordered rows).
-hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, _Float16* dst, hipStream_t s);
-const void* rec_kernel(int HP);
+// W_ih ([4H][K]) of one layer as the projection GEMM's W operand ([4 HP][Kp], lane-ordered rows,
+// zero columns K..Kp-1).
+hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, int Kp, _Float16* dst, hipStream_t s);
+// W_ih of layer 0 (I <= 32) as the recurrent kernel's MFMA A fragments (PackedLayout::wx0).
+hipError_t launch_pack_rec_wx0(const Geometry& g, const _Float16* w_ih0, _Float16* dst, hipStream_t s);
+const void* rec_kernel(int HP, bool x0);
+
+// Time-parallel input projection (plh_gemm.hip): C[m][n] = sum_k X[m][k] W[n][k] for m < M, n < N,
+// fp16 operands and result, fp32 accumulation.  Row-major X [M][ldx], W [N][K], C [M][ldc], or with
+// `blocked` X and C in fragment-blocked order, [M / 16][ld / 32][64 lanes][8] (block (mb, g), lane l:
+// row 16 mb + l % 16, columns 32 g + 8 (l / 16) + 0..7).  K % 128 == 0, K <= 512, N % 128 == 0,
+// ldx >= K and ldc >= N multiples of 8 (blocked: of 32, M % 16 == 0), 16-byte aligned pointers
+// (gemm_shape_ok).  A persistent launch of about one workgroup per CU.
+bool gemm_shape_ok(long long M, int N, int K, long long ldx, long long ldc, bool blocked);
+hipError_t launch_proj_gemm(const _Float16* X, long long ldx, const _Float16* W, int K, _Float16* C, long long ldc,
+                            long long M, int N, bool blocked, int cus, hipStream_t s);
+// Offset (in halfs) of element (row r, column k) of a fragment-blocked [rows / 16][ld / 32][64][8] matrix.
+__host__ __device__ inline size_t blocked_index(size_t r, int k, int ld) {
+  return (((r >> 4) * (size_t)(ld >> 5) + (k >> 5)) * 64 + ((k >> 3) & 3) * 16 + (r & 15)) * 8 + (k & 7);
+}
+double proj_gemm_flops(long long M, int N, int K);
 
 // MFMA rate probe (plh_probe.hip): `blocks` workgroups of 16 waves (one per CU), each wave issuing
 // iters x 8 independent v_mfma_f32_16x16x32_f16; out holds blocks x 1024 floats, clk blocks x 2

@@ -40,6 +40,9 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
   g->kci = HP / 32;
   g->kc = 2 * g->kci;
   g->g_in0 = (I + 7) / 8;
+  g->rec_x0 = (g->rec_ok && I <= 32) ? 1 : 0;
+  g->kp0 = g->rec_x0 ? 0 : (I + 127) / 128 * 128;
+  g->kp = (H + 127) / 128 * 128;
   return true;
 }
 
@@ -48,6 +51,7 @@ Geometry as_layer_sequential(const Geometry& g) {
   r.rec = 1;
   r.slices = Rec<512>::kS;
   r.max_wg_tiles = 1;
+  if (r.rec_x0) r.g_in0 = 4;  // x as one zero-padded MFMA K chunk
   return r;
 }
 
@@ -70,7 +74,9 @@ PackedLayout packed_layout(const Geometry& g) {
   p.wrec = off;
   if (g.rec_ok) off = align256(off + (size_t)g.L * (g.HP / 16) * g.kci * 4 * 64 * 8 * sizeof(_Float16));
   p.wih = off;
-  if (g.rec_ok) off = align256(off + (size_t)4 * g.HP * (g.I + (size_t)(g.L - 1) * g.H) * sizeof(_Float16));
+  if (g.rec_ok) off = align256(off + (size_t)4 * g.HP * (g.kp0 + (size_t)(g.L - 1) * g.kp) * sizeof(_Float16));
+  p.wx0 = off;
+  if (g.rec_ok && g.rec_x0) off = align256(off + (size_t)Rec<512>::kS * 8 * 2 * 64 * 8 * sizeof(_Float16));
   p.total = off;
   return p;
 }
@@ -85,7 +91,8 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   w.counters = 256;
   w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile);
   if (g.rec) {
-    w.hseq = w.xring = w.xp;
+    // xp (rec_x0 only) holds x as [ntile][T][4][16] f16x8
+    w.hseq = w.xring = align256(w.xp + (g.rec_x0 ? ntile * seq_len * 4 * 16 * 16 : 0));
     w.xring_words = ntile * 2 * g.HP * 8;
     w.gates = align256(w.xring + w.xring_words * sizeof(uint64_t));
     w.xs = align256(w.gates + (size_t)seq_len * chunk_rows * 4 * g.HP * sizeof(_Float16));
@@ -100,18 +107,21 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   return w;
 }
 
-static const void* recurrent_kernel(const Geometry& g, int tile_rows, bool ragged, int wg_tiles = 1) {
-  if (g.rec) return tile_rows == 16 && wg_tiles == 1 ? rec_kernel(g.HP) : nullptr;
+static const void* recurrent_kernel(const Geometry& g, int tile_rows, bool ragged, int wg_tiles = 1,
+                                    bool x0 = false) {
+  if (g.rec) return tile_rows == 16 && wg_tiles == 1 ? rec_kernel(g.HP, x0) : nullptr;
   if (g.slices > 1) return tile_rows == 16 ? sliced_kernel(g.HP, wg_tiles) : nullptr;
   return wavefront_kernel(g.HP, tile_rows, ragged);
 }
 
 int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err) {
-  // The smallest occupancy of the variants (with and without lengths, every tile count), so any fits.
+  // The smallest occupancy of the variants (with and without lengths, every tile count, with and
+  // without the in-kernel layer-0 projection), so any fits.
   int cap = 0;
-  for (int v = 0; v < 2 * g.max_wg_tiles; ++v) {
+  for (int v = 0; v < 2 * g.max_wg_tiles * (g.rec ? 2 : 1); ++v) {
     const bool ragged = v & 1;
-    const void* fn = recurrent_kernel(g, tile_rows, ragged, 1 + v / 2);
+    const bool x0 = g.rec && (v / (2 * g.max_wg_tiles)) == 1;
+    const void* fn = recurrent_kernel(g, tile_rows, ragged, 1 + (v / 2) % g.max_wg_tiles, x0);
     if (!fn) {
       *err = hipErrorInvalidValue;
       return 0;
@@ -128,7 +138,7 @@ int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err) {
 }
 
 hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s) {
-  const void* fn = recurrent_kernel(g, a.tile_rows, a.lengths != nullptr, a.wg_tiles);
+  const void* fn = recurrent_kernel(g, a.tile_rows, a.lengths != nullptr, a.wg_tiles, a.wx0 != nullptr);
   if (!fn || a.wg_tiles < 1 || a.ntile % a.wg_tiles) return hipErrorInvalidValue;
   ForwardArgs args = a;
   void* params[] = {&args};

@@ -96,8 +96,6 @@ __global__ void pack_linear_kernel(const _Float16* __restrict__ w, const _Float1
   if (e < O) bl[e] = b ? (float)b[e] : 0.0f;
 }
 
-// x [B, T, I] -> xp [ntile][T][kci0][4][rows] f16x8: B-fragment order for tiles of `rows` rows,
-// zero padded.
 // Forward prologue: x of rows [row0, row_end) into xp (B-fragment order: per tile and step, g0
 // 8-wide K groups of `rows` f16x8, zero past I and past row_end), and the zeroing of up to three
 // u32 ranges (status, counters, exchange ring), in one launch.
@@ -173,15 +171,16 @@ hipError_t launch_pack_linear(const Geometry& g, const _Float16* w, const _Float
   return hipGetLastError();
 }
 
-hipError_t launch_forward_prologue(const Geometry& g, const ForwardArgs& a, uint32_t* status, hipStream_t s) {
-  const size_t npack = (size_t)a.ntile * a.T * g.g_in0 * a.tile_rows;
+hipError_t launch_forward_prologue(const Geometry& g, const ForwardArgs& a, uint32_t* status, int g0,
+                                   size_t ring_words, hipStream_t s) {
+  const size_t npack = (size_t)a.ntile * a.T * g0 * a.tile_rows;
   const size_t nstat = status ? 1 : 0;
   const size_t nctr = (size_t)g.L * a.ntile;
-  const size_t nring = g.slices > 1 ? (size_t)g.L * a.ntile * 2 * g.HP * 8 * 2 : 0;  // u64 words as u32
+  const size_t nring = ring_words * 2;  // u64 words as u32
   const size_t n = std::max(std::max(npack, nstat), std::max(nctr, nring));
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(forward_prologue_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, a.I, a.row0, a.row_end,
-                     a.ntile, a.tile_rows, g.g_in0, a.xp, status, nstat, a.counters, nctr,
+                     a.ntile, a.tile_rows, g0, a.xp, status, nstat, a.counters, nctr,
                      reinterpret_cast<uint32_t*>(a.xring), nring);
   return hipGetLastError();
 }

@@ -3,12 +3,16 @@
 // With [W_ih | W_hh] resident (plh_sliced.hip) a layer of H = 512 needs 16 workgroups per 16-row
 // tile, so a 256-CU device covers 64 rows of all layers per launch.  Here each layer's input
 // projection for all T steps is one GEMM (x_t W_ih^T, fp16 in and out with fp32 accumulation, as
-// the reference's torch::matmul of fp16 tensors; issued by the host, plh_capi.hip) and the
+// the reference's torch::matmul of fp16 tensors; plh_gemm.hip, launched by the host) and the
 // persistent kernel below keeps only W_hh resident: 8 workgroups ("slices") per 16-row tile, 64
 // hidden units each, so one launch covers 512 rows of one layer.  The layers run one after another.
+// Layer 0 with I <= 32 needs no GEMM: its x_t W_ih^T is one K chunk of MFMAs inside the kernel (the
+// X0 variant), from x packed in B-fragment order, so nothing of size T x rows x 4H is written.
 //   * the GEMM's output columns are in lane order: W_ih's rows are permuted (and padded to 4 HP) at
 //     pack time so that the 8 projections one lane needs per step (4 gates x 2 units) are 16
-//     contiguous bytes, one load, issued two steps ahead;
+//     contiguous bytes, one load, issued two steps ahead; projections and layer inputs are kept
+//     fragment-blocked (1 KB per 16 rows x 32 columns), so a wave's projection load and the
+//     GEMM's stores and loads each move one contiguous 1 KB block;
 //   * wave w of a slice holds the i, f, g, o rows of W_hh for unit group w % 4 (16 units) and the
 //     K half w / 4 of h_{t-1}: 8 K-chunks x 4 gates of MFMA A fragments (128 VGPRs);
 //   * per step each wave computes its partial gate sums from h_{t-1} in LDS (32 MFMAs), the two
@@ -52,32 +56,46 @@ __host__ __device__ constexpr int rec_gate_col(int slice, int wave, int kgx) {
   return ((slice * 8 + wave) * 4 + kgx) * 8;
 }
 
-// W_ih ([4H][K], torch layout) as the GEMM's A operand [4 HP][K] with rows in lane order (the
-// inverse of rec_gate_col) and zero rows for padded units.
-__global__ void pack_rec_wih_kernel(const _Float16* __restrict__ w_ih, int H, int HP, int K,
+// W_ih ([4H][K], torch layout) as the GEMM's W operand [4 HP][Kp] with rows in lane order (the
+// inverse of rec_gate_col), zero rows for padded units and zero columns K..Kp-1.
+__global__ void pack_rec_wih_kernel(const _Float16* __restrict__ w_ih, int H, int HP, int K, int Kp,
                                     _Float16* __restrict__ dst) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (size_t)4 * HP * K) return;
-  const int col = (int)(e / K), k = (int)(e % K);
+  if (e >= (size_t)4 * HP * Kp) return;
+  const int col = (int)(e / Kp), k = (int)(e % Kp);
   const int q = (col & 7) >> 1, j = col & 1, kgx = (col >> 3) & 3, wave = (col >> 5) & 7, slice = col >> 8;
   const int u = slice * 64 + (wave & 3) * 16 + kgx * 4 + 2 * (wave >> 2) + j;
-  dst[e] = u < H ? w_ih[((size_t)q * H + u) * K + k] : (_Float16)0.0f;
+  dst[e] = (u < H && k < K) ? w_ih[((size_t)q * H + u) * K + k] : (_Float16)0.0f;
 }
 
-// x rows [row0, row_end) into [T][rows_pad][HP] (the first GEMM's input, K = I columns used).
-__global__ void rec_input_kernel(const _Float16* __restrict__ x, int T, int I, int row0, int row_end, int rows_pad,
-                                 int HP, _Float16* __restrict__ xs) {
+// W_ih of layer 0 (I <= 32) as MFMA A fragments of the X0 kernel: [8 slices][8 waves][2][64 lanes][8];
+// wave w holds gates 2 (w / 4) and 2 (w / 4) + 1 of unit group w % 4 (lane l: unit row l % 16, k =
+// 8 (l / 16) + 0..7), so the two K-half waves of a group share the four gates.
+__global__ void pack_rec_wx0_kernel(const _Float16* __restrict__ w_ih, int H, int I, _Float16* __restrict__ dst) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (size_t)T * rows_pad * I) return;
-  const int i = (int)(e % I);
-  const size_t tb = e / I;
+  if (e >= (size_t)Rec<512>::kS * 8 * 2 * 64 * 8) return;
+  const int jj = e & 7, lane = (e >> 3) & 63, j = (e >> 9) & 1, wv = (e >> 10) & 7, sl = (int)(e >> 13);
+  const int u = sl * Rec<512>::kHs + (wv & 3) * 16 + (lane & 15);
+  const int q = 2 * (wv >> 2) + j, k = (lane >> 4) * 8 + jj;
+  dst[e] = (u < H && k < I) ? w_ih[((size_t)q * H + u) * I + k] : (_Float16)0.0f;
+}
+
+// x rows [row0, row_end) into the first GEMM's input, fragment-blocked [T * rows_pad][HP] (row
+// t * rows_pad + b): columns 0..KP-1, zero past I and past the launch's rows.
+__global__ void rec_input_kernel(const _Float16* __restrict__ x, int T, int I, int row0, int row_end, int rows_pad,
+                                 int HP, int KP, _Float16* __restrict__ xs) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (size_t)T * rows_pad * KP) return;
+  const int i = (int)(e % KP);
+  const size_t tb = e / KP;
   const int b = (int)(tb % rows_pad);
   const int t = (int)(tb / rows_pad);
   const int r = row0 + b;
-  xs[tb * HP + i] = r < row_end ? x[((size_t)r * T + t) * I + i] : (_Float16)0.0f;
+  xs[blocked_index(tb, i, HP)] = (r < row_end && i < I) ? x[((size_t)r * T + t) * I + i] : (_Float16)0.0f;
 }
 
-template <int HP>
+// X0: layer 0 with I <= 32, its input projection computed here from xp (a.gates unused).
+template <int HP, bool X0>
 __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   using C = Rec<HP>;
   constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch, KCW = C::kKcw;
@@ -96,6 +114,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   sliced_coords(blockIdx.x, a.ntile, S, a.xcd_map, unused_layer, tile, slice);
   const int layer = a.layer;
   const int g = wave & 3, e = wave >> 2;  // unit group, K half
+  const bool e0 = __builtin_amdgcn_readfirstlane(e) == 0;
   const int en = lane & 15, kgx = lane >> 4;
   // This lane's units eu, eu + 1 of row en: elements 2e, 2e + 1 of lane `lane` of the group's D
   // fragments (units 4 kgx + i, row en).
@@ -131,6 +150,13 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     for (int kc = 0; kc < KCW; ++kc)
 #pragma unroll
       for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
+  }
+  // X0: W_ih of layer 0 for gates 2e, 2e + 1 of this wave's unit group.
+  f16x8 wx[2] = {};
+  if constexpr (X0) {
+    const f16x8* p = reinterpret_cast<const f16x8*>(a.wx0) + (size_t)(slice * 8 + wave) * 2 * 64 + lane;
+    wx[0] = p[0];
+    wx[1] = p[64];
   }
   // The resident weights complete here (otherwise the compiler keeps them "possibly outstanding"
   // and waits for every global access in flight before the step loop's MFMAs).
@@ -170,9 +196,18 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // 2 q + j is gate q of unit eu + j.  Padded units read zero columns and padded rows zero inputs.
   // One unconditional 16-byte load (a load under an exec branch makes the compiler wait for it
   // together with the ring poll), consumed two steps after it is issued.
-  const _Float16* gsrc = a.gates + b * (size_t)(4 * HP) + rec_gate_col(slice, wave, kgx);
+  // X0: instead, x of step min(t, Tt - 1) as this lane's MFMA B fragment (row en, k 8 kgx .. +7) from
+  // xp ([ntile][T][4][16] f16x8).
+  // Blocked projections: step t's 16 rows of this tile are block row t * ntile + tile; this lane's
+  // 16 bytes are lane kgx * 16 + en of column block rec_gate_col(...) / 32 = slice * 8 + wave.
+  const f16x8* gsrc = X0 ? nullptr
+                         : reinterpret_cast<const f16x8*>(a.gates) + ((size_t)tile * (4 * HP / 32) + slice * 8 + wave) * 64 +
+                               kgx * 16 + en;
+  const f16x8* xsrc = X0 ? a.xp + (size_t)tile * a.T * 64 + kgx * 16 + en : nullptr;
   auto gload = [&](int t) -> f16x8 {
-    return *reinterpret_cast<const f16x8*>(gsrc + (size_t)(t < Tt ? t : Tt - 1) * a.rows_pad * (4 * HP));
+    const size_t tc = (size_t)(t < Tt ? t : Tt - 1);
+    if constexpr (X0) return xsrc[tc * 64];
+    return gsrc[tc * a.ntile * (4 * HP / 32) * 64];
   };
 
   // Packed exchange.  A word carries 4 fp16 of one row: the pair of a lane with even kgx (units
@@ -235,22 +270,34 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
 
   uint64_t wv[NW];
   // The next layer's input: h_t of this slice's 64 units x 16 rows, written a step later from
-  // hbuf as 128 contiguous 16-byte runs (each row's 128 bytes whole) instead of 4-byte pieces.
+  // hbuf in 16-byte pieces, fragment-blocked: two contiguous 1 KB blocks (row block t * ntile + tile,
+  // column blocks 2 slice and 2 slice + 1), one per wave.
   constexpr int kCopyThreads = HS * 16 / 8;
   const int copy_row = threadIdx.x & 15, copy_k8 = slice * (HS / 8) + (threadIdx.x >> 4) % (HS / 8);
   const int copy_src = copy_k8 * 16 + copy_row;  // f16x8 index of (row, units 8 copy_k8 ..) in hbuf
-  auto copy_out = [&](int t, const f16x8& v) {
-    *reinterpret_cast<f16x8*>(a.hout + ((size_t)t * a.rows_pad + tile * 16 + copy_row) * HP + copy_k8 * 8) = v;
-  };
-  // One step: h_{t-1} in hbuf -> h_t in hbuf; gp holds the input projection of step t and is
-  // reloaded with that of step t + 2; gq holds that of step t + 1.  Returns false if a wait failed.
+  f16x8* const copy_dst = last ? nullptr
+                               : reinterpret_cast<f16x8*>(a.hout) + ((size_t)tile * (HP / 32) + (copy_k8 >> 2)) * 64 +
+                                     (copy_k8 & 3) * 16 + copy_row;
+  auto copy_out = [&](int t, const f16x8& v) { copy_dst[(size_t)t * a.ntile * (HP / 32) * 64] = v; };
+  // One step: h_{t-1} in hbuf -> h_t in hbuf; gp holds the input projection of step t (X0: x_t)
+  // and is reloaded with that of step t + 2; gq holds that of step t + 1.  Returns false if a wait
+  // failed.
   auto step = [&](int t, f16x8& gp, f16x8& gq) -> bool {
-    // Partial gate sums of this wave's K half of h_{t-1}.
+    // Partial gate sums of this wave's K half of h_{t-1} (X0: plus x_t W_ih^T of its two gates).
     {
       const f16x8* src = hbuf + e * KCW * FV + lane;
       f32x4 acc[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (X0) {
+        if (e0) {
+          acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[0], gp, acc[0], 0, 0, 0);
+          acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[1], gp, acc[1], 0, 0, 0);
+        } else {
+          acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[0], gp, acc[2], 0, 0, 0);
+          acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[1], gp, acc[3], 0, 0, 0);
+        }
+      }
 #pragma unroll
       for (int kc = 0; kc < KCW; ++kc) {
         const f16x8 bv = src[kc * FV];
@@ -273,8 +320,8 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float2 bv = s_bias[q][(eu - slice * HS) >> 1];
-        z[q][0] = bv.x + (float)gp[2 * q];
-        z[q][1] = bv.y + (float)gp[2 * q + 1];
+        z[q][0] = X0 ? bv.x : bv.x + (float)gp[2 * q];
+        z[q][1] = X0 ? bv.y : bv.y + (float)gp[2 * q + 1];
 #pragma unroll
         for (int ee = 0; ee < 2; ++ee) {
           const float2 v = reinterpret_cast<const float2*>(&part[ee * 4 + g][q][lane])[e];
@@ -494,22 +541,31 @@ hipError_t launch_pack_rec_layer(const Geometry& g, int layer, const _Float16* w
   return hipGetLastError();
 }
 
-hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, _Float16* dst, hipStream_t s) {
-  const size_t n = (size_t)4 * g.HP * K;
-  hipLaunchKernelGGL(pack_rec_wih_kernel, blocks_for(n, 256), 256, 0, s, w_ih, g.H, g.HP, K, dst);
+hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, int Kp, _Float16* dst, hipStream_t s) {
+  const size_t n = (size_t)4 * g.HP * Kp;
+  hipLaunchKernelGGL(pack_rec_wih_kernel, blocks_for(n, 256), 256, 0, s, w_ih, g.H, g.HP, K, Kp, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_rec_wx0(const Geometry& g, const _Float16* w_ih0, _Float16* dst, hipStream_t s) {
+  if (g.HP != 512 || g.I > 32) return hipErrorInvalidValue;
+  const size_t n = (size_t)Rec<512>::kS * 8 * 2 * 64 * 8;
+  hipLaunchKernelGGL(pack_rec_wx0_kernel, blocks_for(n, 256), 256, 0, s, w_ih0, g.H, g.I, dst);
   return hipGetLastError();
 }
 
 hipError_t launch_rec_input(const Geometry& g, const ForwardArgs& a, _Float16* xs0, hipStream_t s) {
-  const size_t n = (size_t)a.T * a.rows_pad * g.I;
+  const size_t n = (size_t)a.T * a.rows_pad * g.kp0;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(rec_input_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, g.I, a.row0, a.row_end, a.rows_pad,
-                     g.HP, xs0);
+                     g.HP, g.kp0, xs0);
   return hipGetLastError();
 }
 
-const void* rec_kernel(int HP) {
-  return HP == 512 ? reinterpret_cast<const void*>(&lstm_rec_kernel<512>) : nullptr;
+const void* rec_kernel(int HP, bool x0) {
+  if (HP != 512) return nullptr;
+  return x0 ? reinterpret_cast<const void*>(&lstm_rec_kernel<512, true>)
+            : reinterpret_cast<const void*>(&lstm_rec_kernel<512, false>);
 }
 
 }  // namespace plh

@@ -66,6 +66,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plh_set_wait_limit_us.argtypes = [_i64]
     lib.plh_probe_mfma_f16.restype = _i32
     lib.plh_probe_mfma_f16.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+    lib.plh_input_projection.restype = _i32
+    lib.plh_input_projection.argtypes = [_vp, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp]
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -325,6 +327,60 @@ class NativeLibrary:
         ghz = ctypes.c_double(0.0)
         self._check(self.lib.plh_probe_mfma_f16(ctypes.byref(tf), ctypes.byref(ghz)), "plh_probe_mfma_f16")
         return float(tf.value), float(ghz.value)
+
+    # ---- the time-parallel input projection GEMM ---------------------------------------------
+    def input_projection(self, x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                         blocked: bool = False) -> torch.Tensor:
+        """out[m, n] = sum_k x[m, k] w[n, k] (fp16 MFMA GEMM, fp32 accumulation, fp16 result).
+
+        Row-major (blocked=False): x [rows, K] fp16 with unit column stride (its row stride may exceed
+        K), out [rows, cols].  Fragment-blocked (blocked=True): x is a contiguous [rows, ldx] tensor
+        in the layout of `to_blocked` (the first K columns are used), out likewise [rows, cols]
+        blocked.  w: [cols, K] fp16; K % 128 == 0, K <= 512, cols % 128 == 0.  Replaces the
+        reference's torch::matmul input projection (persistent_lstm_hip.cu:2988-2994).  Launched on
+        the current stream."""
+        for name, t in (("x", x), ("w", w)):
+            if t.dim() != 2 or t.dtype != torch.float16 or t.device.type != "cuda":
+                raise ValueError(f"{name} must be a 2-D float16 HIP tensor")
+        w = w.contiguous()
+        cols, k = int(w.size(0)), int(w.size(1))
+        rows = int(x.size(0))
+        if blocked:
+            if not x.is_contiguous():
+                raise ValueError("a blocked x must be contiguous")
+            ldx = int(x.size(1))
+        else:
+            if x.stride(1) != 1 or (rows > 1 and x.stride(0) < x.size(1)):
+                raise ValueError("x must have unit column stride and row stride >= its width")
+            if int(x.size(1)) != k:
+                raise ValueError("x and w must have the same K")
+            ldx = int(x.stride(0)) if rows > 1 else k
+        if out is None:
+            out = torch.empty((rows, cols), dtype=torch.float16, device=x.device)
+        elif (tuple(out.shape) != (rows, cols) or out.dtype != torch.float16 or out.stride(1) != 1
+              or (blocked and not out.is_contiguous())):
+            raise ValueError("out must be a float16 [rows, cols] tensor with unit column stride (blocked: contiguous)")
+        ldo = cols if (blocked or rows <= 1) else int(out.stride(0))
+        with torch.cuda.device(x.device):
+            rc = self.lib.plh_input_projection(x.data_ptr(), ldx, w.data_ptr(), k, out.data_ptr(), ldo, rows, cols,
+                                               1 if blocked else 0, _stream(x.device))
+        self._check(rc, "plh_input_projection")
+        return out
+
+    @staticmethod
+    def to_blocked(t: torch.Tensor) -> torch.Tensor:
+        """[rows, ld] (rows % 16 == 0, ld % 32 == 0) -> the fragment-blocked layout of the same shape:
+        element (r, c) at (((r / 16) (ld / 32) + c / 32) 64 + ((c % 32) / 8) 16 + r % 16) 8 + c % 8."""
+        rows, ld = int(t.size(0)), int(t.size(1))
+        if rows % 16 or ld % 32:
+            raise ValueError("blocked layouts need rows % 16 == 0 and columns % 32 == 0")
+        return t.reshape(rows // 16, 16, ld // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(rows, ld).contiguous()
+
+    @staticmethod
+    def from_blocked(t: torch.Tensor) -> torch.Tensor:
+        """Inverse of to_blocked."""
+        rows, ld = int(t.size(0)), int(t.size(1))
+        return t.reshape(rows // 16, ld // 32, 4, 16, 8).permute(0, 3, 1, 2, 4).reshape(rows, ld).contiguous()
 
     # ---- reference extension surface (bindings.cpp:154-165) ----------------------------------
     def repeat_first_row(self, inp: torch.Tensor, output_batch_size: int) -> torch.Tensor:

@@ -16,6 +16,7 @@ Numerics: fp16 weights/activations, fp32 accumulation, fp32 c, fp16 h per step, 
 from __future__ import annotations
 
 import os
+import weakref
 from typing import Any, Optional, Sequence, Tuple
 
 import torch
@@ -81,14 +82,27 @@ class NativeModuleFallback(nn.Module):
         return self.module(*args, **kwargs)
 
 
-def _param_key(tensors: Sequence[Optional[torch.Tensor]]) -> tuple:
-    key = []
-    for t in tensors:
-        if t is None:
-            key.append(None)
-        else:
-            key.extend((id(t), t.device.type, t.device.index, str(t.dtype), t._version))
-    return tuple(key)
+class _TensorSetKey:
+    """Identity of a list of tensors for a cache: the same live objects (weak references, so an id
+    reused by a later object never matches) with unchanged version counters, storage, dtype and
+    device."""
+
+    def __init__(self, tensors: Sequence[Optional[torch.Tensor]]):
+        self._refs = [None if t is None else weakref.ref(t) for t in tensors]
+        self._sig = self.signature(tensors)
+
+    @staticmethod
+    def signature(tensors: Sequence[Optional[torch.Tensor]]) -> tuple:
+        return tuple(None if t is None else (t._version, t.data_ptr(), tuple(t.shape), str(t.dtype), t.device.type,
+                                             t.device.index) for t in tensors)
+
+    def matches(self, tensors: Sequence[Optional[torch.Tensor]]) -> bool:
+        if len(tensors) != len(self._refs):
+            return False
+        for r, t in zip(self._refs, tensors):
+            if (r is None) != (t is None) or (r is not None and r() is not t):
+                return False
+        return self.signature(tensors) == self._sig
 
 
 class PersistentLSTM(nn.Module):
@@ -111,7 +125,8 @@ class PersistentLSTM(nn.Module):
             if self.bias:
                 setattr(self, f"bias_ih_l{l}", nn.Parameter(layer.bias_ih))
                 setattr(self, f"bias_hh_l{l}", nn.Parameter(layer.bias_hh))
-        self._pack_key: Optional[tuple] = None
+        self._pack_key: Optional[_TensorSetKey] = None
+        self._pack_device: Optional[tuple] = None
         self._pack_blob: Optional[torch.Tensor] = None
 
     @classmethod
@@ -144,8 +159,8 @@ class PersistentLSTM(nn.Module):
             params.extend(self.layer_params(l))
         if linear is not None:
             params.extend([linear.weight, linear.bias])
-        key = (device.type, device.index) + _param_key(params)
-        if self._pack_key != key or self._pack_blob is None:
+        dev = (device.type, device.index)
+        if self._pack_blob is None or self._pack_device != dev or not self._pack_key.matches(params):
             ext = require_extension()
             lw = [self.layer_params(l) for l in range(self.num_layers)]
             self._pack_blob = ext.pack(
@@ -155,7 +170,8 @@ class PersistentLSTM(nn.Module):
                 linear.weight if linear is not None else None,
                 linear.bias if linear is not None else None,
             )
-            self._pack_key = key
+            self._pack_key = _TensorSetKey(params)
+            self._pack_device = dev
         return self._pack_blob
 
     def forward(self, x, hx: Optional[Tuple[torch.Tensor, torch.Tensor]] = None):
@@ -193,7 +209,10 @@ class PersistentLSTMRegressor(nn.Module):
             self.linear.weight.copy_(packed.linear_weight)
             if packed.linear_bias is not None:
                 self.linear.bias.copy_(packed.linear_bias)
-        self._uniform_key: Optional[tuple] = None
+        # Uniform-batch decision of the last input: a weak reference to that tensor object and its
+        # signature (version counter, shape, strides, offset, dtype, device).
+        self._uniform_ref: Optional[weakref.ref] = None
+        self._uniform_sig: Optional[tuple] = None
         self._uniform_value = False
         self._debug_reported = False
 
@@ -219,8 +238,16 @@ class PersistentLSTMRegressor(nn.Module):
         return True if ext is None else ext.supports(*self.dims())
 
     def _should_use_uniform_batch_fast_path(self, x: torch.Tensor) -> bool:
-        """Same contract as model.py:493-520: env PERSISTENT_LSTM_HIP_UNIFORM_BATCH = auto (detect,
-        cached per input version) | 1 (assume) | 0 (off)."""
+        """Same contract as model.py:493-520: env PERSISTENT_LSTM_HIP_UNIFORM_BATCH = auto (detect) |
+        1 (assume) | 0 (off).
+
+        In auto mode the decision (a device comparison plus a host sync) is reused only for the same
+        live tensor object with an unchanged version counter, shape, strides and offset.  The
+        reference keys it on data_ptr and _version (model.py:506-520); that key repeats when a fresh
+        tensor lands on a freed block of the caching allocator (factory tensors start at version 0),
+        which would broadcast row 0 of a non-uniform input.  A weak reference cannot: once the tensor
+        it saw is freed it resolves to None.  Writes that bypass the version counter (`.data`, raw
+        pointers) are not seen, as in the reference."""
         mode = os.environ.get("PERSISTENT_LSTM_HIP_UNIFORM_BATCH", "auto").strip().lower()
         if mode in _OFF or x.dim() != 3 or x.size(0) <= 1:
             return False
@@ -228,12 +255,14 @@ class PersistentLSTMRegressor(nn.Module):
             return True
         if mode not in _AUTO:
             raise ValueError("PERSISTENT_LSTM_HIP_UNIFORM_BATCH must be one of: auto, detect, assume, 1, 0")
-        key = (x.data_ptr(), x.device.type, x.device.index, str(x.dtype), tuple(x.size()), tuple(x.stride()),
-               x._version)
-        if self._uniform_key != key:
+        sig = (x._version, tuple(x.size()), tuple(x.stride()), x.storage_offset(), str(x.dtype), x.device.type,
+               x.device.index)
+        seen = self._uniform_ref() if self._uniform_ref is not None else None
+        if seen is not x or self._uniform_sig != sig:
             with torch.no_grad():
                 self._uniform_value = bool(torch.equal(x, x.narrow(0, 0, 1).expand_as(x)))
-            self._uniform_key = key
+            self._uniform_ref = weakref.ref(x)
+            self._uniform_sig = sig
         return self._uniform_value
 
     def _check_input(self, x: torch.Tensor) -> None:

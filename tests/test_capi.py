@@ -63,15 +63,21 @@ def test_supported_geometries(ext, I, H, L, O, ok):
 def test_packed_bytes_closed_form(ext):
     # wpack: L * (HP/16 waves) * (2*HP/32 chunks) * 4 gates * 64 lanes * 16 B, then f32 bias, head, all 256-aligned
     a = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    r128 = lambda v: (v + 127) // 128 * 128  # noqa: E731
     for I, H, L, O, HP in [(5, 128, 4, 24, 128), (5, 100, 2, 3, 128), (5, 40, 3, 7, 64), (5, 10, 1, 0, 32),
-                           (5, 256, 4, 24, 256), (5, 200, 2, 3, 256), (5, 512, 4, 24, 512), (7, 400, 1, 1, 512)]:
+                           (5, 256, 4, 24, 256), (5, 200, 2, 3, 256), (5, 512, 4, 24, 512), (7, 400, 1, 1, 512),
+                           (40, 300, 3, 2, 512)]:
         wp = L * (HP // 16) * (HP // 16) * 4 * 64 * 16
         want = a(wp) + a(L * 4 * HP * 4) + a(O * HP * 4) + a(O * 4)
         if HP == 512:
-            # both paths' operands: the layer-sequential kernel's W_hh fragments (half of the above) and
-            # W_ih of every layer as its projection GEMM's operand, padded to 4 HP rows ([4HP][I], then
-            # [4HP][H])
-            want += a(wp // 2) + a(4 * HP * (I + (L - 1) * H) * 2)
+            # both paths' operands: the layer-sequential kernel's W_hh fragments (half of the above);
+            # W_ih of every layer its projection GEMM computes, [4HP][K padded to 128] - layer 0 only when
+            # I > 32, else layer 0's W_ih as the recurrent kernel's MFMA fragments (8 slices x 8 waves x
+            # 2 gates x 64 lanes x 16 B)
+            kp0 = 0 if I <= 32 else r128(I)
+            want += a(wp // 2) + a(4 * HP * (kp0 + (L - 1) * r128(H)) * 2)
+            if I <= 32:
+                want += a(8 * 8 * 2 * 64 * 16)
         assert ext.packed_bytes(I, H, L, O) == want
     with pytest.raises(ValueError):
         ext.packed_bytes(5, 1000, 4, 24)
@@ -109,15 +115,21 @@ def test_layer_sequential_workspace_layout(ext):
     # HP = 512 with a batch that needs several wavefront launches (8 of 64 rows here) runs layer by
     # layer: 8 workgroups per 16-row tile hold one layer's W_hh, so 256 / 8 = 32 tiles (512 rows) fit
     # one launch.  The workspace holds one layer's input projection for every
-    # step (fp16 [T][rows][4HP]), two alternating fp16 layer-input buffers [T][rows][HP] and one
-    # layer's exchange ring (tiles * 2 * HP * 8 words of 8 bytes).
+    # step (fp16 [T][rows][4HP]), two alternating fp16 layer-input buffers [T][rows][HP], one
+    # layer's exchange ring (tiles * 2 * HP * 8 words of 8 bytes) and, since I <= 32 puts layer 0's
+    # projection inside the recurrent kernel, x as one zero-padded 32-wide MFMA K chunk per row and
+    # step (64 bytes).
     L, T, H = 4, 1000, 512
     rows = 512
     b = ext.workspace_bytes(5, H, L, 24, 512, T)
     gates = T * rows * 4 * H * 2
     xs = 2 * T * rows * H * 2
     ring = (rows // 16) * 2 * H * 8 * 8
-    assert gates + xs + ring <= b < gates + xs + ring + (1 << 12)
+    xp = rows * T * 64
+    assert gates + xs + ring + xp <= b < gates + xs + ring + xp + (1 << 12)
+    # I > 32: layer 0's projection is a GEMM too (x goes to the first xs buffer): no packed x
+    b40 = ext.workspace_bytes(40, H, L, 24, 512, T)
+    assert gates + xs + ring <= b40 < gates + xs + ring + (1 << 12)
     # a padded H (400 -> 512) is sized by HP throughout
     assert ext.workspace_bytes(5, 400, L, 24, 512, T) == b
     # sequences whose projections would exceed 24 GiB stay on the wavefront path (64 rows per launch:

@@ -152,6 +152,16 @@ int plh_kernel_timing_read(double* total_ms, int* forwards);
  */
 int plh_set_wait_limit_us(int64_t limit_us);
 
+/*
+ * Failure injection for tests of the failure path: with step >= 0, the calling thread's later
+ * plh_forward calls that run the layer-sequential path make one workgroup of each launch treat its
+ * exchange wait at that step as timed out (PLH_STATUS_TIMEOUT, outputs NaN where not computed, every
+ * kernel still ends normally).  step < 0 turns it off.  The other paths' first hand-off wait can be
+ * made to time out with a small plh_set_wait_limit_us; this path's per-step waits finish too fast
+ * for that.  No counterpart in the reference.
+ */
+int plh_inject_wait_failure(int step);
+
 /* out[r, c] = in[0, c] for r < rows (fp16).  Replaces repeat_first_row
  * (bindings.cpp:164, persistent_lstm_hip.cu:1684-1695, :1784-1809). */
 int plh_repeat_first_row(const void* in, void* out, int rows, int cols, void* stream);

@@ -14,7 +14,9 @@
  *   - Linear head on the last step of the last layer:
  *       persistent_lstm_reference.cpp:61-63, reference.py:66-72
  *   - optional initial state hx = (h0, c0) of shape [L, B, H]: reference.py:29-32
- *   - "reference device numerics" mode (numerics = 1) restating the reference kernels' storage:
+ *   - "reference device numerics" mode (numerics = 1, and 2 with an fp16 input projection as the
+ *     reference's generic path computes it, persistent_lstm_hip.cu:2988-2994) restating the
+ *     reference kernels' storage:
  *       bias fused as one fp16 rounding of (b_ih + b_hh)         model.py:552
  *       h rounded to fp16 after every step, c kept in fp32      persistent_lstm_hip.cu:524-525
  *       sigmoid(x) = 1 / (1 + exp(-x)), tanh                   persistent_lstm_hip.cu:96-98
@@ -115,7 +117,10 @@ enum {
  *            state after p steps (for ragged rows, after min(p, length) steps)
  *   out_seq  [B, T, H] last layer's output sequence (zero where t >= length), or NULL
  *   h_n, c_n [L, B, H] final states, or NULL
- * numerics: 0 = fp32 textbook, 1 = reference device numerics (see header).
+ * numerics: 0 = fp32 textbook, 1 = reference device numerics (see header), 2 = as 1 with the input
+ *           projection W_ih x of every step rounded to fp16 before the bias and recurrent terms are
+ *           added (the reference's generic path: persistent_lstm_hip.cu:2988-2994 computes it as an
+ *           fp16 torch::matmul, the persistent kernel adds the rest in fp32).
  * Returns 0, or -1 for invalid arguments.
  */
 int oracle_lstm_forward(int B, int T, int I, int H, int L, const float* x, const float* const* w_ih,
@@ -174,10 +179,14 @@ int oracle_lstm_forward(int B, int T, int I, int H, int L, const float* x, const
         for (int t = 0; t < T; ++t) {
           if (t < len) {
             for (int g = 0; g < G; ++g) {
-              double a = bl[g];
               const float* wi = Wi + (size_t)g * K;
               const float* xt = in + (size_t)t * Kmax;
-              for (int k = 0; k < K; ++k) a += (double)wi[k] * (double)xt[k];
+              double p = 0.0;
+              for (int k = 0; k < K; ++k) p += (double)wi[k] * (double)xt[k];
+              /* numerics 2: the input projection is an fp16 tensor (the reference's generic path,
+                 torch::matmul of fp16 operands, persistent_lstm_hip.cu:2988-2994) */
+              if (numerics == 2) p = (double)oracle_round_half((float)p);
+              double a = bl[g] + p;
               if (mutation != MUT_DROP_RECURRENT) {
                 if (mutation == MUT_TRANSPOSE_WHH) {
                   for (int j = 0; j < H; ++j) a += (double)Wh[(size_t)j * G + g] * (double)h[j];

@@ -5,9 +5,12 @@ TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.
 cpu_baseline leg, always as the checker.  The product package never imports this module.
 
 Numerics modes (see the header of lstm_oracle.c for the reference file:line of each rule):
-  "fp32"     -- textbook fp32 LSTM (what torch's CPU nn.LSTM computes), double accumulation
-  "ref_fp16" -- the reference kernels' storage: fp16-rounded fused bias, fp16 h every step,
-                fp32 c, fp16 head output.  Inputs/weights are rounded to fp16 by this wrapper.
+  "fp32"          -- textbook fp32 LSTM (what torch's CPU nn.LSTM computes), double accumulation
+  "ref_fp16"      -- the reference kernels' storage: fp16-rounded fused bias, fp16 h every step,
+                     fp32 c, fp16 head output.  Inputs/weights are rounded to fp16 by this wrapper.
+  "ref_fp16_proj" -- as ref_fp16, with each step's input projection W_ih x rounded to fp16 before
+                     the bias and recurrent terms are added (the reference's generic path, whose
+                     projection is an fp16 torch::matmul).
 """
 from __future__ import annotations
 
@@ -119,15 +122,15 @@ def lstm_forward(
     [P,L,B,H] for probe_steps.
     """
     lib = _load()
-    mode = {"fp32": 0, "ref_fp16": 1}[numerics]
+    mode = {"fp32": 0, "ref_fp16": 1, "ref_fp16_proj": 2}[numerics]
     x = _f32(x)
     if x.ndim != 3:
         raise ValueError("x must be [B, T, I]")
     B, T, I = x.shape
     L = len(layers)
     H = int(np.asarray(layers[0][1]).shape[1])
-    conv = round_half if mode == 1 else _f32
-    if mode == 1:
+    conv = round_half if mode else _f32
+    if mode:
         x = round_half(x)
     keep: List[np.ndarray] = []
     wi, wh, bi, bh = (_F * L)(), (_F * L)(), (_F * L)(), (_F * L)()
@@ -174,8 +177,10 @@ def lstm_forward(
 
 
 def linear(inp, w, b, numerics: str = "fp32") -> np.ndarray:
+    """bias + inp w^T (double accumulation); "ref_fp16": operands rounded to fp16 and the result
+    rounded to fp16 as the reference's head kernel does (persistent_lstm_hip.cu:1662-1682)."""
     lib = _load()
-    mode = {"fp32": 0, "ref_fp16": 1}[numerics]
+    mode = {"fp32": 0, "ref_fp16": 1, "ref_fp16_proj": 1}[numerics]
     conv = round_half if mode == 1 else _f32
     inp, w = conv(inp), conv(w)
     b = conv(b) if b is not None else None

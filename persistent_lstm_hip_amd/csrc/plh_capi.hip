@@ -157,6 +157,8 @@ KernelTiming& timing() {
 // Bound on inter-workgroup waits of this thread's forwards (plh_set_wait_limit_us).
 constexpr int64_t kDefaultWaitUs = 2000000;
 thread_local int64_t g_wait_us = kDefaultWaitUs;
+// Failure injection of this thread's forwards (plh_inject_wait_failure); -1: off.
+thread_local int g_fail_step = -1;
 
 // Compute units of the current device (the persistent projection GEMM's grid), queried once per
 // device.
@@ -331,6 +333,7 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   a.O = g.O;
   a.g_in0 = g.g_in0;
   a.wait_ticks = (uint64_t)g_wait_us * 100u;  // s_memrealtime: 100 MHz
+  a.fail_step = g_fail_step;
 
   KernelTiming& tm = timing();
   const bool timed = tm.used * 2 < (int)tm.ev.size();
@@ -468,6 +471,11 @@ int plh_status(const void* workspace, uint32_t* status, void* stream) {
 
 int plh_set_wait_limit_us(int64_t limit_us) {
   g_wait_us = limit_us > 0 ? limit_us : kDefaultWaitUs;
+  return PLH_OK;
+}
+
+int plh_inject_wait_failure(int step) {
+  g_fail_step = step >= 0 ? step : -1;
   return PLH_OK;
 }
 

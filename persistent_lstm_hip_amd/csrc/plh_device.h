@@ -19,9 +19,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // e^{-k z} as 2^(min(-k z log2 e, 40)) on v_exp_f32.  The cap keeps a product of three (1 + e)
 // factors below 2^121 (no overflow) and moves no gate by more than 1e-12 (logistic(-27.7) ~ 1e-12).
+// The minimum is IEEE 754-2019 `minimum` (v_minimum3_f32), which returns NaN for a NaN argument, so a
+// NaN pre-activation gives a NaN gate as torch does (fminf would return the cap).
 constexpr float kExpCap = 40.0f;
 __device__ __forceinline__ float exp_neg(float z, float k) {
-  return __builtin_amdgcn_exp2f(fminf(z * (-k * kLog2e), kExpCap));
+  return __builtin_amdgcn_exp2f(__builtin_elementwise_minimum(z * (-k * kLog2e), kExpCap));
 }
 
 // One LSTM cell update (torch gate order i, f, g, o) from the pre-activations and the old c, with
@@ -72,6 +74,29 @@ __device__ __attribute__((unused)) int wait_counter(const uint32_t* ctr, uint32_
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
+}
+
+// After a failed wait: NaN into every output element a lane owns, units u0 .. u0 + n - 1 of batch row
+// `grow` in `layer`: h_n, c_n, every probe and, for the last layer, every step of out_seq.  With the
+// head poisoned as well, each output element of a forward is then either its correct value or NaN.
+__device__ __attribute__((unused)) void poison_lane_outputs(const ForwardArgs& a, int layer, int grow, int u0, int n,
+                                                            bool last) {
+  const float qnan = __builtin_nanf("");
+  const _Float16 hnan = (_Float16)qnan;
+  for (int j = 0; j < n; ++j) {
+    const int u = u0 + j;
+    if (u >= a.H) continue;
+    const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
+    if (a.h_n) a.h_n[si] = hnan;
+    if (a.c_n) a.c_n[si] = hnan;
+    for (int p = 0; p < a.n_probe; ++p) {
+      const size_t o = (((size_t)p * a.L + layer) * a.B + grow) * a.H + u;
+      a.probe_h[o] = qnan;
+      a.probe_c[o] = qnan;
+    }
+    if (last && a.out_seq)
+      for (int t = 0; t < a.T; ++t) a.out_seq[((size_t)grow * a.T + t) * a.H + u] = hnan;
+  }
 }
 
 // Offset (in halfs) of element (row r, k) in a fragment-ordered [ROWS x K] block: the block of K

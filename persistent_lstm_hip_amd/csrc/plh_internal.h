@@ -112,6 +112,8 @@ struct ForwardArgs {
   int g_in0;                    // 8-wide K groups of x per step in xp
   int xcd_map;                  // 1: keep a tile's layer chain on one XCD
   uint64_t wait_ticks;          // bound on one inter-workgroup wait, in s_memrealtime ticks (100 MHz)
+  int fail_step;                // failure injection (plh_inject_wait_failure): the layer-sequential kernel's
+                                // workgroup 0 fails its wait at this step; -1: never
   int wg_tiles;                 // sliced kernels: 16-row tiles per workgroup (1 or 2); ntile is a multiple
   // layer-sequential kernel (one layer per launch):
   int layer;                    // the layer this launch runs

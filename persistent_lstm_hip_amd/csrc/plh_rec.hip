@@ -421,6 +421,13 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // the empty asm tells the compiler, which would otherwise wait for every load in flight at
     // the next step's gate math.  Then the projection of step t + 2, issued after the poll (the
     // compiler waits for every load in flight where the poll's retry path joins).
+    // Failure injection for tests (plh_inject_wait_failure): workgroup 0 treats this step's wait as
+    // timed out; its siblings then find the status word set while they wait for its next words.
+    if (t == a.fail_step && blockIdx.x == 0) {
+      s_fail = 1;
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_or(a.status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     asm volatile("" : "+v"(gq));
     gp = gload(t + 2);
     uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf);
@@ -472,7 +479,9 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   if (ok && !last && Tt > 0 && threadIdx.x < kCopyThreads) copy_out(Tt - 1, hbuf[copy_src]);
 
   if (!ok) {
-    // A wait failed (the status word records it): poison this tile's head outputs and leave.
+    // A wait failed, here or in an earlier layer's launch (the status word records it): poison every
+    // output of this workgroup (states, probes, output sequence, head) and leave.
+    if (row_ok) poison_lane_outputs(a, layer, grow, eu, 2, last);
     if (last && slice == 0 && a.out) {
       for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
         const int gr = a.row0 + tile * 16 + idx / a.O;

@@ -490,6 +490,12 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   }
 
   if (!ok) {
+    // A wait failed: poison every output of this workgroup (states, probes, output sequence, head).
+    if (active) {
+#pragma unroll
+      for (int i = 0; i < NTI; ++i)
+        if (row_ok[i]) poison_lane_outputs(a, layer, grow[i], eu, 2, !has_down);
+    }
     if (!has_down && slice == 0 && a.out) {
       for (int idx = threadIdx.x; idx < NTI * 16 * a.O; idx += NT) {
         const int gr = a.row0 + tile0 * 16 + idx / a.O;

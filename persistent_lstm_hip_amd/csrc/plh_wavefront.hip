@@ -399,8 +399,9 @@ lstm_wavefront_kernel(ForwardArgs a) {
     if (!step(t, t - nfull * CH, nfull, false)) ok = false;
 
   if (!ok) {
-    // A hand-off wait failed (the status word records it and fails every other wait): poison this
-    // tile's head outputs and leave.
+    // A hand-off wait failed (the status word records it and fails every other wait): poison every
+    // output of this workgroup (states, probes, output sequence, head) and leave.
+    if (row_ok) poison_lane_outputs(a, layer, grow, uo, UPL, !has_down);
     if (!has_down && a.out) {
       for (int idx = threadIdx.x; idx < ROWS * a.O; idx += NT) {
         const int g = a.row0 + tile * ROWS + idx / a.O;

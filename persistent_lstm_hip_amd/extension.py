@@ -64,6 +64,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plh_repeat_first_row.argtypes = [_vp, _vp, _i32, _i32, _vp]
     lib.plh_set_wait_limit_us.restype = _i32
     lib.plh_set_wait_limit_us.argtypes = [_i64]
+    lib.plh_inject_wait_failure.restype = _i32
+    lib.plh_inject_wait_failure.argtypes = [_i32]
     lib.plh_probe_mfma_f16.restype = _i32
     lib.plh_probe_mfma_f16.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
     lib.plh_input_projection.restype = _i32
@@ -208,11 +210,13 @@ class NativeLibrary:
         want_state: bool = False,
         probe_steps: Optional[Sequence[int]] = None,
         check_status: bool = False,
+        outputs: Optional[Dict[str, torch.Tensor]] = None,
     ) -> Dict[str, torch.Tensor]:
         """Run plh_forward.  dims = (I, H, L, O).  x: [B, T, I] on a HIP device (cast to fp16).
 
         Returns a dict with "out" [B, O], "out_seq" [B, T, H], "h_n"/"c_n" [L, B, H] (fp16) and
-        "probe_h"/"probe_c" [P, L, B, H] (fp32), as requested.
+        "probe_h"/"probe_c" [P, L, B, H] (fp32), as requested.  `outputs` may supply any of these
+        tensors (contiguous, right shape, dtype and device) to be written instead of new ones.
         """
         I, H, L, O = (int(d) for d in dims)
         if not isinstance(x, torch.Tensor) or x.dim() != 3:
@@ -227,10 +231,21 @@ class NativeLibrary:
         B, T = int(x.size(0)), int(x.size(1))
         xh = x.to(torch.float16).contiguous()
         opts = dict(device=device, dtype=torch.float16)
-        out = torch.empty((B, O), **opts) if (want_out and O > 0) else None
-        out_seq = torch.empty((B, T, H), **opts) if want_seq else None
-        h_n = torch.empty((L, B, H), **opts) if want_state else None
-        c_n = torch.empty((L, B, H), **opts) if want_state else None
+        given = dict(outputs or {})
+
+        def buf(name, shape, dtype=torch.float16):
+            t = given.pop(name, None)
+            if t is None:
+                return torch.empty(shape, device=device, dtype=dtype)
+            if tuple(t.shape) != tuple(shape) or t.dtype != dtype or t.device != device or not t.is_contiguous():
+                raise ValueError(f"outputs[{name!r}] must be a contiguous {dtype} tensor of shape {tuple(shape)} "
+                                 f"on {device}")
+            return t
+
+        out = buf("out", (B, O)) if (want_out and O > 0) else None
+        out_seq = buf("out_seq", (B, T, H)) if want_seq else None
+        h_n = buf("h_n", (L, B, H)) if want_state else None
+        c_n = buf("c_n", (L, B, H)) if want_state else None
         lens_dev = None
         if lengths is not None:
             # Host lengths (a list or CPU tensor, as torch.nn.utils.rnn.pack_padded_sequence takes
@@ -260,8 +275,10 @@ class NativeLibrary:
             raise ValueError(f"probe steps must lie in [1, {T}]")
         P = len(probes)
         probe_dev = torch.tensor(probes, dtype=torch.int32, device=device) if P else None
-        probe_h = torch.empty((P, L, B, H), device=device, dtype=torch.float32) if P else None
-        probe_c = torch.empty((P, L, B, H), device=device, dtype=torch.float32) if P else None
+        probe_h = buf("probe_h", (P, L, B, H), torch.float32) if P else None
+        probe_c = buf("probe_c", (P, L, B, H), torch.float32) if P else None
+        if given:
+            raise ValueError(f"outputs given for ones not requested: {sorted(given)}")
         if packed.device != device:
             raise ValueError("packed weights and x must be on the same device")
         with torch.cuda.device(device):
@@ -307,6 +324,11 @@ class NativeLibrary:
         """Bound on inter-workgroup waits of this thread's later forwards (None: the 2 s default)."""
         us = 0 if seconds is None else max(1, int(round(seconds * 1e6)))
         self._check(self.lib.plh_set_wait_limit_us(us), "plh_set_wait_limit_us")
+
+    def inject_wait_failure(self, step: Optional[int]) -> None:
+        """Failure injection for tests (this thread): layer-sequential forwards fail one workgroup's
+        wait at `step` (None: off)."""
+        self._check(self.lib.plh_inject_wait_failure(-1 if step is None else int(step)), "plh_inject_wait_failure")
 
     # ---- timing of the persistent kernel alone ----------------------------------------------
     def kernel_timing(self, max_forwards: int) -> None:
@@ -396,13 +418,34 @@ class NativeLibrary:
         self._check(rc, "plh_repeat_first_row")
         return out
 
+    def _packed_for(self, w_ih: Sequence[torch.Tensor], w_hh: Sequence[torch.Tensor], bias: Sequence[torch.Tensor],
+                    linear_weight: torch.Tensor, linear_bias: Optional[torch.Tensor], source: tuple) -> torch.Tensor:
+        """Packed weights for torch-layout parameters, cached on the identity and version of the
+        tensors the caller passed (`source`): the reference's dispatcher passes the same cached
+        tensors to every forward (model.py:542-582), so they are packed once per weight version."""
+        from .model import _TensorSetKey  # noqa: PLC0415 (model imports this module)
+
+        key = getattr(self, "_compat_key", None)
+        if key is None or not key.matches(source):
+            self._compat_blob = self.pack(w_ih, w_hh, bias, None, linear_weight, linear_bias)
+            self._compat_key = _TensorSetKey(source)
+        return self._compat_blob
+
     def persistent_lstm_regressor_forward_generic_projected(
         self, x, weight_ih: List[torch.Tensor], weight_hh: List[torch.Tensor], bias: List[torch.Tensor],
         linear_weight: torch.Tensor, linear_bias: torch.Tensor,
     ) -> torch.Tensor:
-        """bindings.cpp:163: (x, [W_ih], [W_hh], [b_ih + b_hh], W_lin, b_lin) -> [B, O].  Packs per call."""
-        packed = self.pack(weight_ih, weight_hh, bias, None, linear_weight, linear_bias)
-        dims = (int(weight_ih[0].shape[1]), int(weight_hh[0].shape[1]), len(weight_ih), int(linear_weight.shape[0]))
+        """bindings.cpp:163: (x, [W_ih], [W_hh], [b_ih + b_hh], W_lin, b_lin) -> [B, O]."""
+        return self._forward_torch_layout(x, list(weight_ih), list(weight_hh), list(bias), linear_weight, linear_bias,
+                                          tuple(weight_ih) + tuple(weight_hh) + tuple(bias) + (linear_weight, linear_bias))
+
+    def _forward_torch_layout(self, x, w_ih, w_hh, bias, linear_weight, linear_bias, source) -> torch.Tensor:
+        if not isinstance(x, torch.Tensor) or x.dim() != 3:
+            raise ValueError("x must be a [batch, seq_len, input_size] tensor")
+        if not (len(w_ih) == len(w_hh) == len(bias)) or not w_ih:
+            raise ValueError("weight_ih, weight_hh and bias need one tensor per layer")
+        packed = self._packed_for(w_ih, w_hh, bias, linear_weight, linear_bias, source)
+        dims = (int(w_ih[0].shape[1]), int(w_hh[0].shape[1]), len(w_ih), int(linear_weight.shape[0]))
         return self.forward(packed, dims, x)["out"]
 
     @staticmethod
@@ -415,35 +458,80 @@ class NativeLibrary:
         full = packed.permute(0, 2, 1).reshape(pairs * 2, out)
         return full[:k].t().contiguous()
 
-    def persistent_lstm4_forward_interleaved(self, x, *args) -> torch.Tensor:
-        """bindings.cpp:157: (x, W_ih_l0, W_hh_l0, b_l0, ..., W_ih_l3, W_hh_l3, b_l3, W_lin, b_lin) with
-        kpairs-packed weights (model.py:562-578) and fused biases."""
+    @staticmethod
+    def _four_layers(args) -> None:
         if len(args) != 14:
-            raise ValueError("expected 12 per-layer tensors plus linear weight and bias")
+            raise ValueError("expected 12 per-layer tensors (weight_ih, weight_hh, bias for 4 layers) plus the "
+                             "linear weight and bias")
+
+    def persistent_lstm4_forward(self, x, *args) -> torch.Tensor:
+        """bindings.cpp:155: torch-layout weights [4H, K] and fused biases, 4 layers."""
+        self._four_layers(args)
+        return self._forward_torch_layout(x, [args[3 * l] for l in range(4)], [args[3 * l + 1] for l in range(4)],
+                                          [args[3 * l + 2] for l in range(4)], args[12], args[13], args)
+
+    def persistent_lstm4_forward_packed(self, x, *args) -> torch.Tensor:
+        """bindings.cpp:156: transposed weights W^T [K, 4H] (persistent_lstm_hip.cu:2005-2018) and fused
+        biases, 4 layers."""
+        self._four_layers(args)
+        return self._forward_torch_layout(x, [args[3 * l].t() for l in range(4)], [args[3 * l + 1].t() for l in range(4)],
+                                          [args[3 * l + 2] for l in range(4)], args[12], args[13], args)
+
+    def persistent_lstm4_forward_interleaved(self, x, *args) -> torch.Tensor:
+        """bindings.cpp:157: kpairs-packed W_ih and W_hh (model.py:562-578) and fused biases."""
+        self._four_layers(args)
         H = int(args[1].size(1)) // 4
         I = int(x.size(2))
-        w_ih = [self.unpack_kpairs(args[3 * l], I if l == 0 else H) for l in range(4)]
-        w_hh = [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)]
-        bias = [args[3 * l + 2] for l in range(4)]
-        return self.persistent_lstm_regressor_forward_generic_projected(x, w_ih, w_hh, bias, args[12], args[13])
+        return self._forward_torch_layout(
+            x, [self.unpack_kpairs(args[3 * l], I if l == 0 else H) for l in range(4)],
+            [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)], [args[3 * l + 2] for l in range(4)],
+            args[12], args[13], args)
+
+    def persistent_lstm4_forward_monolithic(self, x, *args) -> torch.Tensor:
+        """bindings.cpp:162: the interleaved arguments (the reference's all-layers-in-one-kernel variant,
+        persistent_lstm_hip.cu:2823-2921); here the same single path as every other entry point."""
+        return self.persistent_lstm4_forward_interleaved(x, *args)
 
     def persistent_lstm4_forward_projected(self, x, *args) -> torch.Tensor:
         """bindings.cpp:158: native W_ih [4H, K] with kpairs-packed W_hh (model.py:548-560)."""
-        if len(args) != 14:
-            raise ValueError("expected 12 per-layer tensors plus linear weight and bias")
+        self._four_layers(args)
         H = int(args[0].size(0)) // 4
-        w_ih = [args[3 * l] for l in range(4)]
-        w_hh = [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)]
-        bias = [args[3 * l + 2] for l in range(4)]
-        return self.persistent_lstm_regressor_forward_generic_projected(x, w_ih, w_hh, bias, args[12], args[13])
+        return self._forward_torch_layout(
+            x, [args[3 * l] for l in range(4)], [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)],
+            [args[3 * l + 2] for l in range(4)], args[12], args[13], args)
 
-    def persistent_lstm4_forward(self, x, *args) -> torch.Tensor:
-        """bindings.cpp:155: torch-layout weights and fused biases."""
-        if len(args) != 14:
-            raise ValueError("expected 12 per-layer tensors plus linear weight and bias")
-        return self.persistent_lstm_regressor_forward_generic_projected(
-            x, [args[3 * l] for l in range(4)], [args[3 * l + 1] for l in range(4)],
-            [args[3 * l + 2] for l in range(4)], args[12], args[13])
+    def persistent_lstm4_forward_projected_uniform(self, x, virtual_batch_size: int, *args) -> torch.Tensor:
+        """bindings.cpp:159: the projected arguments for ONE sequence x [1, T, I] -> [1, O] (the caller
+        broadcasts it with repeat_first_row).  The reference runs `virtual_batch_size` redundant copies
+        of that sequence (persistent_lstm_hip.cu:2399-2549); they change nothing in the result, so one
+        row is computed.  Like the reference, any other x (or virtual_batch_size <= 0) takes the
+        ordinary projected forward of every row (cu:2416-2433)."""
+        return self.persistent_lstm4_forward_projected(x, *args)
+
+    def persistent_lstm4_forward_projected_uniform_p4(self, x, virtual_batch_size: int, *args) -> torch.Tensor:
+        """bindings.cpp:160: as persistent_lstm4_forward_projected_uniform (the reference's 4-way K
+        partition of the same recurrence, persistent_lstm_hip.cu:2551-2685)."""
+        return self.persistent_lstm4_forward_projected_uniform(x, virtual_batch_size, *args)
+
+    def persistent_lstm4_forward_projected_uniform_p8(self, x, virtual_batch_size: int, *args) -> torch.Tensor:
+        """bindings.cpp:161: as persistent_lstm4_forward_projected_uniform (8-way K partition there,
+        persistent_lstm_hip.cu:2687-2821)."""
+        return self.persistent_lstm4_forward_projected_uniform(x, virtual_batch_size, *args)
+
+
+# The reference extension's exported names (bindings.cpp:154-165), in its order.
+REFERENCE_ENTRY_POINTS = (
+    "persistent_lstm4_forward",
+    "persistent_lstm4_forward_packed",
+    "persistent_lstm4_forward_interleaved",
+    "persistent_lstm4_forward_projected",
+    "persistent_lstm4_forward_projected_uniform",
+    "persistent_lstm4_forward_projected_uniform_p4",
+    "persistent_lstm4_forward_projected_uniform_p8",
+    "persistent_lstm4_forward_monolithic",
+    "persistent_lstm_regressor_forward_generic_projected",
+    "repeat_first_row",
+)
 
 
 def library_path() -> str:

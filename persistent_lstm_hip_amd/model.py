@@ -43,6 +43,16 @@ def _debug() -> bool:
     return os.environ.get("PERSISTENT_LSTM_HIP_DEBUG", "0") == "1"
 
 
+def _check_after(ext, device: torch.device) -> None:
+    """With PERSISTENT_LSTM_HIP_CHECK_STATUS=1, every module forward synchronises its stream and
+    raises RuntimeError if the kernel reported a failure (a timed-out wait between workgroups).
+    Off by default: the check costs a host synchronisation per forward.  Either way a failed
+    forward's outputs are NaN where they could not be computed, never stale memory, and
+    `load_extension().check_status(device)` reports it."""
+    if os.environ.get("PERSISTENT_LSTM_HIP_CHECK_STATUS", "0") == "1":
+        ext.check_status(device)
+
+
 class StandardLSTMRegressor(nn.Module):
     """nn.LSTM(batch_first=True) + nn.Linear on the last step (reference model.py:30-45)."""
 
@@ -191,6 +201,7 @@ class PersistentLSTM(nn.Module):
         blob = self.packed_blob(x.device)
         res = ext.forward(blob, (self.input_size, self.hidden_size, self.num_layers, 0), x, lengths=lengths,
                           h0=h0, c0=c0, want_out=False, want_seq=True, want_state=True)
+        _check_after(ext, x.device)
         out, h_n, c_n = res["out_seq"].to(dtype), res["h_n"].to(dtype), res["c_n"].to(dtype)
         if packed_in:
             out = pack_padded_sequence(out, lengths, batch_first=True, enforce_sorted=False)
@@ -286,6 +297,7 @@ class PersistentLSTMRegressor(nn.Module):
             out = ext.repeat_first_row(row, batch)
         else:
             out = ext.forward(blob, self.dims(), x)["out"]
+        _check_after(ext, x.device)
         return out if x.dtype == torch.float16 else out.to(x.dtype)
 
     def forward_ragged(self, x: torch.Tensor, lengths) -> torch.Tensor:
@@ -295,6 +307,7 @@ class PersistentLSTMRegressor(nn.Module):
         self._check_input(x)
         blob = self.lstm.packed_blob(x.device, self.linear)
         out = ext.forward(blob, self.dims(), x, lengths=lengths)["out"]
+        _check_after(ext, x.device)
         return out if x.dtype == torch.float16 else out.to(x.dtype)
 
     def forward_probe(self, x: torch.Tensor, steps: Sequence[int], lengths=None):
@@ -304,6 +317,7 @@ class PersistentLSTMRegressor(nn.Module):
         self._check_input(x)
         blob = self.lstm.packed_blob(x.device, self.linear)
         res = ext.forward(blob, self.dims(), x, lengths=lengths, probe_steps=steps)
+        _check_after(ext, x.device)
         return res["out"], res["probe_h"], res["probe_c"]
 
 

@@ -418,19 +418,27 @@ def test_layer_sequential_zero_lengths_large_state_and_nan(gpu):
     np.testing.assert_array_equal(res_n["out"].cpu().numpy()[others], res_c["out"].cpu().numpy()[others])
 
 
-@pytest.mark.parametrize("H,B", [(128, 16), (256, 16), (256, 600)])
+@pytest.mark.parametrize("H,B", [(128, 16), (256, 16), (256, 600), (512, 600)])
 def test_wait_timeout_is_reported_and_recovers(gpu, H, B):
     """A forced 1 us wait bound: the next layer's first hand-off wait cannot be met, so the kernel sets
     the timeout status, poisons the outputs and ends; the front end raises; the default bound then
     gives correct results again (the status word is cleared by every forward).  (256, 600) runs the
-    two-tile sliced workgroups."""
+    two-tile sliced workgroups, (512, 600) the layer-sequential path.
+
+    Every output element of the timed-out forward - output sequence, final states, probes, head -
+    is either NaN (the workgroups whose waits failed poison all their outputs) or its correct value
+    (workgroups that completed before the failure); none holds stale memory."""
     I, L, O, T = 5, 2, 3, 64
     _say(f"forced wait timeout H={H} B={B}")
     native = make_regressor(I, H, L, O)
     x = make_x(B, T, I)
     model = _gpu_model(native)
     xg = x.to("cuda", torch.float16)
-    gpu.set_wait_limit(1e-6)
+    # The layer-sequential path's per-step waits end within microseconds, too soon for any bound:
+    # its failure is injected at step 5 instead.
+    force = (lambda: gpu.inject_wait_failure(5)) if H == 512 else (lambda: gpu.set_wait_limit(1e-6))
+    unforce = (lambda: gpu.inject_wait_failure(None)) if H == 512 else (lambda: gpu.set_wait_limit(None))
+    force()
     try:
         out = model(xg)
         torch.cuda.synchronize()
@@ -438,11 +446,41 @@ def test_wait_timeout_is_reported_and_recovers(gpu, H, B):
             gpu.check_status(torch.device("cuda"))
         assert torch.isnan(out.float()).any(), "a timed-out forward must poison its outputs"
     finally:
-        gpu.set_wait_limit(None)
+        unforce()
     got = model(xg)
     gpu.check_status(torch.device("cuda"))
     want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear))
     assert_close(got.float().cpu().numpy(), want, what="after timeout")
+
+    # every requested output of a timed-out forward: NaN or correct (outputs pre-filled with 7.0 so
+    # that an element nobody wrote would show)
+    blob = model.lstm.packed_blob(xg.device, model.linear)
+    ref = oracle.lstm_forward(x.numpy(), oracle_layers(native.lstm), probe_steps=(1, T // 2, T), want_seq=True)
+    force()
+    try:
+        P = 3
+        fill = {"out": torch.full((B, O), 7.0, device="cuda", dtype=torch.float16),
+                "out_seq": torch.full((B, T, H), 7.0, device="cuda", dtype=torch.float16),
+                "h_n": torch.full((L, B, H), 7.0, device="cuda", dtype=torch.float16),
+                "c_n": torch.full((L, B, H), 7.0, device="cuda", dtype=torch.float16),
+                "probe_h": torch.full((P, L, B, H), 7.0, device="cuda"),
+                "probe_c": torch.full((P, L, B, H), 7.0, device="cuda")}
+        res = gpu.forward(blob, (I, H, L, O), xg, want_seq=True, want_state=True, probe_steps=(1, T // 2, T),
+                          outputs=fill)
+        torch.cuda.synchronize()
+        with pytest.raises(RuntimeError, match="timed out"):
+            gpu.check_status(torch.device("cuda"))
+    finally:
+        unforce()
+    nan_seen = False
+    w_head = oracle.linear(ref["h_n"][-1], *linear_params(native.linear))
+    for k, w in (("out_seq", ref["out_seq"]), ("h_n", ref["h_n"]), ("c_n", ref["c_n"]), ("probe_h", ref["probe_h"]),
+                 ("probe_c", ref["probe_c"]), ("out", w_head)):
+        g = res[k].float().cpu().numpy()
+        bad = ~np.isnan(g) & (np.abs(g - w) > 2e-2)
+        assert not bad.any(), f"{k}: {int(bad.sum())} elements neither NaN nor correct"
+        nan_seen |= bool(np.isnan(g).any())
+    assert nan_seen, "a timed-out forward must poison the outputs it could not compute"
 
 
 @pytest.mark.parametrize("I,H,L,O,B,T,zero_tail", [

@@ -184,10 +184,13 @@ def test_half_conversion_matches_numpy():
         np.testing.assert_array_equal(oracle.round_half(arr), arr.astype(np.float16).astype(np.float32))
 
 
-def test_ref_fp16_mode_matches_stepwise_torch_emulation():
-    """numerics='ref_fp16' (fp16-rounded fused bias and h, fp32 c) against an independent torch
-    LSTMCell loop that rounds the same quantities."""
-    I, H, B, T = 5, 32, 3, 40
+@pytest.mark.parametrize("mode", ["ref_fp16", "ref_fp16_proj"])
+def test_ref_fp16_modes_match_stepwise_torch_emulation(mode):
+    """numerics='ref_fp16' (fp16-rounded fused bias and h, fp32 c) and 'ref_fp16_proj' (plus the
+    fp16-rounded input projection) against an independent torch LSTMCell loop that rounds the same
+    quantities.  With I = 40 inputs of magnitude ~1 the projection rounding moves gates by ~1e-3, so
+    dropping it (or applying it in the wrong mode) fails the c bound."""
+    I, H, B, T = 40, 32, 3, 40
     lstm = _torch_lstm(I, H, 1, seed=21)
     x = make_x(B, T, I).half().float()
     w_ih, w_hh, b_ih, b_hh = (getattr(lstm, f"{n}_l0").detach().half().float()
@@ -196,14 +199,35 @@ def test_ref_fp16_mode_matches_stepwise_torch_emulation():
     h = torch.zeros(B, H)
     c = torch.zeros(B, H)
     for t in range(T):
-        z = x[:, t].double() @ w_ih.double().t() + h.double() @ w_hh.double().t() + bias.double()
+        p = x[:, t].double() @ w_ih.double().t()
+        if mode == "ref_fp16_proj":
+            p = p.float().half().double()
+        z = p + h.double() @ w_hh.double().t() + bias.double()
         i, f, g, o = z.chunk(4, dim=1)
         c = (torch.sigmoid(f) * c.double() + torch.sigmoid(i) * torch.tanh(g)).float()
         h = (torch.sigmoid(o) * torch.tanh(c.double())).float().half().float()
-    r = oracle.lstm_forward(x.numpy(), [tuple(t.numpy() for t in (w_ih, w_hh, b_ih, b_hh))], numerics="ref_fp16")
+    layers = [tuple(t.numpy() for t in (w_ih, w_hh, b_ih, b_hh))]
+    r = oracle.lstm_forward(x.numpy(), layers, numerics=mode)
     np.testing.assert_allclose(r["h_n"][0], h.numpy(), atol=1e-3)
     np.testing.assert_allclose(r["c_n"][0], c.numpy(), atol=1e-5)
     assert np.abs(r["h_n"][0] - h.numpy()).mean() < 1e-5
+    other = oracle.lstm_forward(x.numpy(), layers, numerics="ref_fp16_proj" if mode == "ref_fp16" else "ref_fp16")
+    assert np.abs(other["c_n"][0] - c.numpy()).max() > 1e-5, "the two modes must differ measurably"
+
+
+def test_linear_modes_match_float64():
+    """oracle.linear: fp32 mode = float64 product rounded to float32; ref_fp16 = operands rounded to
+    fp16, float64 product rounded through float32 to fp16 (the reference head's fp16 output)."""
+    rng = np.random.default_rng(9)
+    inp = rng.normal(size=(7, 33)).astype(np.float32)
+    w = (rng.normal(size=(5, 33)) / 4).astype(np.float32)
+    b = rng.normal(size=5).astype(np.float32)
+    want32 = (inp.astype(np.float64) @ w.T.astype(np.float64) + b).astype(np.float32)
+    np.testing.assert_array_equal(oracle.linear(inp, w, b), want32)
+    h = lambda a: a.astype(np.float16).astype(np.float64)  # noqa: E731
+    want16 = (h(inp) @ h(w).T + h(b)).astype(np.float32).astype(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(oracle.linear(inp, w, b, numerics="ref_fp16"), want16)
+    assert not np.array_equal(oracle.linear(inp, w, b, numerics="ref_fp16"), want32)
 
 
 @pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (needs the reference checkout)")

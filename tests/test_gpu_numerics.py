@@ -1,0 +1,186 @@
+"""Numerics of the kernels' cell update and a tight regression bound on whole forwards.
+
+1. The cell's own sigmoid/tanh (exp2 + reciprocal in a combined rational form, plh_device.h) through
+   the real kernels, no extra ABI: one layer, T = 1, W_hh = 0, and per hidden unit a crafted input
+   weight, bias and c0 so that one activation of a known argument lands in an observable output:
+     unit 0  c_1 = sigmoid(z)        z = x (W_ih of gate i = 1), f = -30, g = +30
+     unit 1  c_1 = tanh(z)           z = x (W_ih of gate g = 1), i = +30, f = -30
+     unit 2  h_1 = sigmoid(z)        z = x (W_ih of gate o = 1), i = -30, f = +30, c0 = 20
+     unit 3  h_1 = tanh(c0)          c0 = x, i = -30, f = +30, o = +30
+   c_1 is read in fp32 (probe_c), h_1 as rounded to fp16 (probe_h).  Rows sweep every finite fp16
+   value of x (units 0-2) and every fp16 value of c0 including +-inf and NaN (unit 3; x is finite on
+   every row, since a non-finite x would reach every gate through the zero weights, 0 * inf = NaN,
+   as in torch); extra units carry extreme values (+-65504, +-inf, NaN, +-1e4) in their biases.  Reference: float64 sigmoid and tanh.  Recorded: max
+   abs error and max fp32 ulp error (c_1), and fp16 ulp error (h_1).  The reference's own device math
+   is 1/(1+expf(-x)) and tanhf (persistent_lstm_hip.cu:96-98); torch's fp32 functions are within an
+   ulp or two of float64, so float64 is the stricter yardstick.
+2. Whole forwards against the oracle's restatement of the device rounding (fp16 h every step; with
+   the layer-sequential path also the fp16 input projection): bounds 10-100x below the north star.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close, linear_params, make_lengths, make_regressor, make_x, oracle_layers
+from oracle import oracle
+from persistent_lstm_hip_amd import PersistentLSTMRegressor
+
+pytestmark = pytest.mark.gpu
+
+BIG = 30.0
+
+
+def _say(msg: str) -> None:
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _sigmoid64(z):
+    with np.errstate(over="ignore"):
+        return 1.0 / (1.0 + np.exp(-z))
+
+
+def _fp32_ulp(v):
+    v = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(v, 2.0 ** -126)))
+    return 2.0 ** (e - 23)
+
+
+def _fp16_ulp(v):
+    v = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(v, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def _all_fp16(finite_only: bool) -> np.ndarray:
+    v = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    if finite_only:
+        v = v[np.isfinite(v)]
+    else:
+        v = v[~np.isnan(v)]
+        v = np.concatenate([v, np.float16([np.nan])])
+    return v.astype(np.float32)
+
+
+def _sweep(gpu, H: int):
+    """Returns (x per row, c0 of unit 3 per row, probe_c [B, H], probe_h [B, H], extra-unit specs)."""
+    I, L = 1, 1
+    fin = _all_fp16(finite_only=True)
+    xs = np.concatenate([fin, np.float32([0.0, 0.0, 0.0])])
+    cs = np.concatenate([fin, np.float32([np.inf, -np.inf, np.nan])])
+    B = xs.size
+    w_ih = torch.zeros(4 * H, 1)
+    w_hh = torch.zeros(4 * H, H)
+    b = torch.zeros(4, H)
+    w_ih[0 * H + 0, 0] = 1.0
+    b[1, 0], b[2, 0] = -BIG, BIG
+    w_ih[2 * H + 1, 0] = 1.0
+    b[0, 1], b[1, 1] = BIG, -BIG
+    w_ih[3 * H + 2, 0] = 1.0
+    b[0, 2], b[1, 2] = -BIG, BIG
+    b[0, 3], b[1, 3], b[3, 3] = -BIG, BIG, BIG
+    # extreme arguments through biases: units 4 + 3 j + kind test sigmoid(i) and tanh(g) in c_1 and
+    # sigmoid(o) in h_1 (c0 = 20) of special value j
+    specials = np.float32([0.0, -0.0, 6.0e-8, -6.0e-8, 1e4, -1e4, 65504.0, -65504.0, np.inf, -np.inf, np.nan])
+    n_sp = min(len(specials), (H - 4) // 3)
+    extra = []
+    c0 = torch.zeros(L, B, H)
+    c0[0, :, 2] = 20.0
+    c0[0, :, 3] = torch.from_numpy(cs)
+    for j in range(n_sp):
+        for kind, (gate, others) in enumerate(((0, {1: -BIG, 2: BIG}), (2, {0: BIG, 1: -BIG}),
+                                               (3, {0: -BIG, 1: BIG}))):
+            u = 4 + 3 * j + kind
+            b[gate, u] = float(specials[j])
+            for g_, v in others.items():
+                b[g_, u] = v
+            if kind == 2:
+                c0[0, :, u] = 20.0
+            extra.append((u, kind, float(specials[j])))
+    dev = torch.device("cuda")
+    packed = gpu.pack([w_ih.to(dev)], [w_hh.to(dev)], [b.reshape(-1).to(dev)], None, None, None)
+    xd = torch.from_numpy(xs).reshape(B, 1, 1).to(dev, torch.float16)
+    res = gpu.forward(packed, (I, H, L, 0), xd, c0=c0.to(dev, torch.float16), want_out=False, probe_steps=[1],
+                      check_status=True)
+    return (xs, cs, res["probe_c"][0, 0].cpu().numpy().astype(np.float64),
+            res["probe_h"][0, 0].cpu().numpy().astype(np.float64), extra)
+
+
+@pytest.mark.parametrize("H,path", [(4, "wavefront"), (200, "sliced"), (400, "layer-sequential")])
+def test_cell_activations_against_float64(gpu, H, path):
+    _say(f"activation sweep H={H} ({path})")
+    xs, cs, pc, ph, extra = _sweep(gpu, H)
+    x = xs.astype(np.float64)
+    report = {}
+
+    def c_err(got, want, name):
+        err = np.abs(got - want)
+        big = np.abs(want) >= 2.0 ** -20
+        ulp = (err[big] / _fp32_ulp(want[big])).max()
+        report[name] = (float(err.max()), float(ulp))
+        return err.max(), ulp
+
+    # sigmoid(z) in c_1 (unit 0) and tanh(z) in c_1 (unit 1), z = every finite fp16
+    e_sig, u_sig = c_err(pc[:, 0], _sigmoid64(x), "sigmoid via c")
+    e_tanh, u_tanh = c_err(pc[:, 1], np.tanh(x), "tanh via c")
+    # sigmoid(z) and tanh(c0) in h_1: fp16 ulps against float64
+    c = cs.astype(np.float64)
+    for name, got, want in (("sigmoid via h", ph[:, 2], _sigmoid64(x)), ("tanh(c) via h", ph[:, 3], np.tanh(c))):
+        ok = np.isfinite(want)
+        d = np.abs(got[ok] - want[ok]) / _fp16_ulp(want[ok])
+        report[name] = (float(np.abs(got[ok] - want[ok]).max()), float(d.max()))
+    _say(f"H={H}: " + ", ".join(f"{k}: max_abs {a:.2e} max_ulp {u:.1f}" for k, (a, u) in report.items()))
+    assert e_sig <= 4e-7 and e_tanh <= 4e-7, report
+    assert u_sig <= 16, report  # sigmoid is well conditioned: a few fp32 ulps
+    assert report["sigmoid via h"][1] <= 1.0 and report["tanh(c) via h"][1] <= 1.0, report
+    # tanh(c) of +-inf is +-1, of NaN is NaN (the last three rows of unit 3)
+    assert ph[-3, 3] == 1.0 and ph[-2, 3] == -1.0 and np.isnan(ph[-1, 3])
+    # extreme arguments through the biases
+    for u, kind, v in extra:
+        got = pc[0, u] if kind < 2 else ph[0, u]
+        want = (_sigmoid64(np.float64(v)) if kind != 1 else np.tanh(np.float64(v)))
+        if math.isnan(v):
+            assert math.isnan(got), (u, kind, v, got)
+        else:
+            assert abs(got - want) <= (1e-3 if kind == 2 else 1e-6), (u, kind, v, got, want)
+
+
+def _probe_compare(ph, pc, ref, rows, what, max_h, max_c):
+    for p in range(ref["probe_h"].shape[0]):
+        for name, got, want, bound in (("h", ph, ref["probe_h"], max_h), ("c", pc, ref["probe_c"], max_c)):
+            g = got[p][:, rows].cpu().numpy()
+            mx, mn = assert_close(g, want[p], max_abs=bound, mean_abs=bound / 10, what=f"{what} {name}[{p}]")
+            _say(f"{what} {name} probe {p}: max_abs {mx:.2e} mean_abs {mn:.2e}")
+
+
+@pytest.mark.parametrize("cfg", ["C2", "C5", "H512-wavefront", "H512-layer-sequential"])
+def test_forward_regression_bound_against_device_rounding_oracle(gpu, cfg):
+    """Head output and h/c at steps 1, 100, 1000 against the oracle's restatement of the device
+    rounding (ref_fp16: fp16 h every step, fp32 c; the layer-sequential path additionally rounds
+    the input projection to fp16: ref_fp16_proj).  Measured (MI355X): head <= 6.1e-5, h <= 1.2e-4,
+    c <= 8.3e-5 max-abs at every configuration.  Bounds: head 2e-4, h and c 4e-4 max-abs (the north
+    star allows 2e-2); what remains is fp32 accumulation order and fp16 roundings of h that fall the
+    other way, which the recurrence carries forward."""
+    I, L, O, T = 5, 4, 24, 1000
+    H = 128 if cfg in ("C2", "C5") else 512
+    B = 512 if cfg in ("C2", "C5", "H512-layer-sequential") else 64
+    numerics = "ref_fp16_proj" if cfg == "H512-layer-sequential" else "ref_fp16"
+    _say(f"regression bound {cfg}: H={H} B={B} ({numerics})")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    lengths = make_lengths(B, T, 200) if cfg == "C5" else None
+    model = PersistentLSTMRegressor.from_native_module(native).to("cuda").half().eval()
+    out, ph, pc = model.forward_probe(x.to("cuda", torch.float16), [1, 100, 1000], lengths=lengths)
+    gpu.check_status(torch.device("cuda"))
+    n = 4 if H == 512 else 16
+    rows = np.r_[0:n, B // 2:B // 2 + n, B - n:B]
+    layers = oracle_layers(native.lstm)
+    ref = oracle.lstm_forward(x.numpy()[rows], layers, lengths=None if lengths is None else lengths.numpy()[rows],
+                              numerics=numerics, probe_steps=(1, 100, 1000))
+    head = oracle.linear(ref["h_n"][-1], *linear_params(native.linear), numerics="ref_fp16")
+    mx, mn = assert_close(out.float().cpu().numpy()[rows], head, max_abs=2e-4, mean_abs=2e-5, what=f"{cfg} head")
+    _say(f"{cfg} head vs {numerics}: max_abs {mx:.2e} mean_abs {mn:.2e}")
+    _probe_compare(ph, pc, ref, rows, cfg, max_h=4e-4, max_c=4e-4)

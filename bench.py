@@ -2,6 +2,7 @@
 """Headline benchmark: the stacked nn.LSTM + nn.Linear fp16 forward of BASELINE.json's metric.
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10]
+    python bench.py --sweep [--cases 128:512,256:512,512:512]   # the reference's sweep CSV instead
 
 Workload (configs[1] of BASELINE.json, "C2"): 4-layer LSTM, input 5, hidden 128, Linear 128 -> 24,
 batch 512, seq 1000, fp16 weights/activations with fp32 accumulation, x ~ N(0, 1), PyTorch-default
@@ -10,12 +11,16 @@ are resident in HBM before the timed region.  Timing follows the reference proto
 (LSTM-hip.py:80-91: 10 warm-ups, 100 timed forwards) with HIP events.
 
 Printed: one JSON line with the driver's fields plus
-  roofline     -- the persistent kernel's algorithmic FLOPs per launch / its average duration
-                  (HIP events around the launch, recorded by the library on the launch stream)
-                  against the MI355X dense fp16 MFMA peak;
-  cpu_baseline -- the reference's own CPU path (persistent_lstm_reference.cpp:42-64 compiled into
-                  oracle/_ref) on this host's cores, or the C oracle when that is not built;
-  parity       -- max/mean abs error of the GPU output against that CPU result.
+  roofline         -- the persistent kernel's algorithmic FLOPs per launch / its average duration
+                      (HIP events around the launch, recorded by the library on the launch stream)
+                      against the MI355X dense fp16 MFMA peak;
+  input_projection -- the time-parallel input-projection GEMM (plh_input_projection) timed alone at
+                      the north star's [512000,128]x[128,512] and at C4's [512000,512]x[512,2048];
+  cpu_baseline     -- torch fp32 nn.LSTM + nn.Linear on this host's cores (the CPU reference the north
+                      star names), 1 warm-up + 3 timed forwards of the full C2 batch, median;
+  cpu_reference_aten -- the reference's own ATen CPU path (persistent_lstm_reference.cpp:42-64,
+                      compiled into oracle/_ref) timed the same way, when it is built;
+  parity           -- max/mean abs error of the GPU output against the torch fp32 CPU output.
 """
 from __future__ import annotations
 
@@ -42,11 +47,6 @@ COUNTERS_FILE = os.path.join(ROOT, "profiles", "lstm_wavefront_c2_counters.txt")
 def algorithmic_flops(I, H, L, O, B, T) -> float:
     """Dense-contraction FLOPs of one forward: 2*B*T*4H*[(I+H) + (L-1)*2H] + 2*B*H*O."""
     return 2.0 * B * T * 4 * H * ((I + H) + (L - 1) * 2 * H) + 2.0 * B * H * O
-
-
-def input_projection_flops(I, H, L, B, T) -> float:
-    """FLOPs of the input projections x_t W_ih^T of all layers: 2*B*T*4H*[I + (L-1)*H]."""
-    return 2.0 * B * T * 4 * H * (I + (L - 1) * H)
 
 
 def _profile_value(path, key):
@@ -78,50 +78,88 @@ def cpu_model_name() -> str:
 
 
 def cpu_baseline(native, x_cpu, reps: int = 3):
-    """Time the reference CPU path (or the C oracle) on this host; returns (record, output)."""
+    """torch fp32 nn.LSTM + nn.Linear (the StandardLSTMRegressor) on all host cores, under
+    inference_mode: 1 warm-up + `reps` timed forwards of the full batch, median.  Returns (record,
+    output)."""
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    with torch.inference_mode():
+        out = native(x_cpu)  # warm-up
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            out = native(x_cpu)
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    rec = {
+        "value": B * T / med,
+        "unit": "seq-steps/s",
+        "cores": int(torch.get_num_threads()),
+        "kind": "reference",
+        "path": "torch fp32 nn.LSTM + nn.Linear on the host (the CPU reference the north star names)",
+        "sample": f"the full C2 batch ({B} x {T}), fp32, 1 warm-up + {reps} timed forwards, median "
+                  f"{med:.3f} s/forward; host '{cpu_model_name()}', os.cpu_count()={os.cpu_count()}, "
+                  f"torch.get_num_threads()={torch.get_num_threads()}",
+        "latency_s": med,
+    }
+    return rec, out.numpy()
+
+
+def cpu_reference_aten(native, x_cpu, reps: int = 3):
+    """The reference's own CPU path (persistent_lstm_reference.cpp:42-64, ATen, compiled into
+    oracle/_ref) on the same batch and cores, or None when it is not built."""
     from oracle import oracle
 
+    if not oracle.ref_available():
+        return None
     layers = [tuple(getattr(native.lstm, f"{n}_l{l}").detach().float().numpy()
                     for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")) for l in range(L)]
     lw = native.linear.weight.detach().float().numpy()
     lb = native.linear.bias.detach().float().numpy()
     xs = x_cpu.numpy()
-    if oracle.ref_available():
-        kind, threads = "reference", torch.get_num_threads()
-        run = lambda xx: oracle.ref_regressor_forward(xx, layers, lw, lb, threads=threads)  # noqa: E731
-        rows = B
-    else:
-        kind, threads = "port", oracle.max_threads()
-        run = lambda xx: oracle.regressor_forward(xx, layers, lw, lb, threads=threads)  # noqa: E731
-        rows = 64  # the scalar C port is slower: time a bounded slice of the batch
-    sample = xs[:rows]
-    out = run(sample)  # warm-up
+    threads = torch.get_num_threads()
+    oracle.ref_regressor_forward(xs, layers, lw, lb, threads=threads)
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        out = run(sample)
+        oracle.ref_regressor_forward(xs, layers, lw, lb, threads=threads)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    rec = {
-        "value": rows * T / med,
-        "unit": "seq-steps/s",
-        "cores": int(threads),
-        "kind": kind,
-        "sample": f"{rows} x {T} rows of the C2 batch, fp32, 1 warm-up + {reps} timed forwards, median "
-                  f"{med:.3f} s/forward; host '{cpu_model_name()}', os.cpu_count()={os.cpu_count()}",
-        "latency_s": med,
-    }
-    return rec, out, rows
+    return {"value": B * T / med, "unit": "seq-steps/s", "cores": int(threads), "latency_s": med,
+            "sample": f"the full C2 batch, fp32, 1 warm-up + {reps} timed forwards, median"}
 
 
-def torch_cpu_nn_lstm(native, x_cpu):
-    """torch fp32 nn.LSTM on the host cores (the comparator BASELINE.md names), one timed forward."""
-    with torch.inference_mode():
-        native(x_cpu[:64])
-        t0 = time.perf_counter()
-        native(x_cpu)
-        dt = time.perf_counter() - t0
-    return {"latency_s": dt, "seq_steps_per_s": B * T / dt, "threads": torch.get_num_threads()}
+def input_projection_timing(ext, dev, reps: int = 20, warmup: int = 5) -> dict:
+    """The time-parallel input-projection GEMM alone (fp16 MFMA, fp32 accumulation, fp16 result), in
+    the fragment-blocked layout the layer-sequential path keeps, at the north star's input-GEMM shape
+    [B*T, 128] x [128, 4*128] and at C4's layer shape [B*T, 512] x [512, 4*512]; HIP events on the
+    launch stream, median of `reps`."""
+    res = []
+    for M, K, N in ((B * T, 128, 512), (B * T, 512, 2048)):
+        g = torch.Generator(device=dev).manual_seed(K)
+        x = torch.randn(M, K, device=dev, generator=g).half()
+        w = (torch.randn(N, K, device=dev, generator=g) / 16).half()
+        out = torch.empty(M, N, device=dev, dtype=torch.float16)
+        for _ in range(warmup):
+            ext.input_projection(x, w, out, blocked=True)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        torch.cuda.synchronize()
+        for a, b in ev:
+            a.record()
+            ext.input_projection(x, w, out, blocked=True)
+            b.record()
+        torch.cuda.synchronize()
+        ms = statistics.median(a.elapsed_time(b) for a, b in ev)
+        flops = 2.0 * M * N * K
+        nbytes = 2.0 * (M * K + N * K + M * N)
+        res.append({"shape": f"[{M},{K}]x[{K},{N}]", "ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+                    "frac_of_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
+                    "hbm_GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 8e12})
+        del x, w, out
+    torch.cuda.empty_cache()
+    return {"kernel": "proj_gemm_kernel<true> (plh_gemm.hip)", "measured": res,
+            "note": "timed alone with HIP events; C2 itself computes each step's projection inside the "
+                    "persistent wavefront kernel, C4 runs this GEMM for layers 1-3 (layer 0 in-kernel)"}
 
 
 def uniform_batch_protocol(model, dev, warmup: int, steps: int) -> dict:
@@ -187,6 +225,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10, help="untimed forwards")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline and parity legs")
     ap.add_argument("--no-other-configs", action="store_true", help="skip timing C3, C4 and C5")
+    ap.add_argument("--sweep", action="store_true",
+                    help="print the reference's sweep CSV (hidden,batch,seq,elapsed_s,throughput,kernel) for --cases "
+                         "instead of the JSON line")
+    ap.add_argument("--cases", default="128:512,256:512,512:512", help="hidden:batch[:seq] cases of --sweep")
+    ap.add_argument("--sweep-backend", default="hip", choices=("hip", "native"))
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -197,6 +240,12 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no HIP GPU visible", file=sys.stderr)
         return 1
+    if args.sweep:
+        from persistent_lstm_hip_amd import sweep
+
+        sweep.run(sweep.parse_cases(args.cases, T), backend=args.sweep_backend, iters=args.steps,
+                  warmup=args.warmup)
+        return 0
 
     from persistent_lstm_hip_amd import PersistentLSTMRegressor, StandardLSTMRegressor
     from persistent_lstm_hip_amd.extension import require_extension
@@ -232,6 +281,7 @@ def main() -> int:
     # On-box check of the roofline constant (after the timed region): the dense fp16 MFMA rate this
     # GPU sustains with the kernels' instruction, and the shader clock meanwhile.
     probe_tflops, probe_ghz = ext.probe_mfma_f16()
+    projection = input_projection_timing(ext, dev)
     uniform = uniform_batch_protocol(model, dev, args.warmup, args.steps)
     others = other_configs(dev) if not args.no_other_configs else None
     total_ms = t_all0.elapsed_time(t_all1)
@@ -286,15 +336,7 @@ def main() -> int:
                         "workgroup per CU (plh_probe_mfma_f16); `peak` stays the published 2.5 PFLOP/s",
             },
         },
-        "input_projection": {
-            "fused": True,
-            "note": "the time-parallel input GEMM is fused into the persistent kernel: each step's x_t W_ih^T "
-                    "runs on MFMA, software-pipelined under the previous step's gate math; achieved = its "
-                    "algorithmic FLOPs / the kernel's duration",
-            "flops_per_launch": input_projection_flops(I, H, L, B, T),
-            "achieved_tflops": input_projection_flops(I, H, L, B, T) / (kernel_ms * 1e-3) / 1e12,
-            "frac_of_peak": input_projection_flops(I, H, L, B, T) / (kernel_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
-        },
+        "input_projection": projection,
         "mfma_util": {
             "algorithmic_percent": 100.0 * achieved / PEAK_FP16_TFLOPS,
             "rocprof_busy_percent": _profile_value(COUNTERS_FILE, "MfmaUtil_percent"),
@@ -311,13 +353,12 @@ def main() -> int:
         "other_configs": others,
     }
     if not args.no_cpu_baseline:
-        base, cpu_out, rows = cpu_baseline(native, x_cpu)
+        base, cpu_out = cpu_baseline(native, x_cpu)
         rec["cpu_baseline"] = base
-        got = out.float().cpu().numpy()[:rows]
-        d = np.abs(got - cpu_out)
-        rec["parity"] = {"vs": base["kind"] + " CPU fp32", "rows": rows, "max_abs": float(d.max()),
+        d = np.abs(out.float().cpu().numpy() - cpu_out)
+        rec["parity"] = {"vs": "torch fp32 nn.LSTM on the CPU", "rows": B, "max_abs": float(d.max()),
                          "mean_abs": float(d.mean()), "tolerance": {"max_abs": 2e-2, "mean_abs": 2e-3}}
-        rec["torch_cpu_nn_lstm"] = torch_cpu_nn_lstm(native, x_cpu)
+        rec["cpu_reference_aten"] = cpu_reference_aten(native, x_cpu)
     else:
         rec["cpu_baseline"] = None
     print(json.dumps(rec), flush=True)

@@ -127,6 +127,24 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
 int plh_input_projection(const void* x, int64_t ldx, const void* w, int k, void* out, int64_t ldo, int64_t rows,
                          int cols, int blocked, void* stream);
 
+/*
+ * plh_forward without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid allocation).  It uses a device
+ * scratch array inside the library, PLH_NOALLOC_SCRATCH_BYTES (64 MiB, plh_noalloc_scratch_bytes()),
+ * one per GPU, held until the process ends; it calls no allocating routine.  A forward whose
+ * plh_workspace_bytes(...) exceeds it is rejected with PLH_ERR_INVALID before anything is enqueued
+ * (e.g. the C2 shape fits up to about 64 rows at 1000 steps).  All calls on one GPU share its scratch:
+ * calls that overlap on one GPU (different streams or threads) race; calls ordered on one stream do
+ * not.  Everything the kernels read from the scratch is written or cleared by the same call.
+ * No counterpart in the reference; outputs and arguments as plh_forward.
+ */
+#define PLH_NOALLOC_SCRATCH_BYTES ((int64_t)64 << 20)
+int plh_forward_noalloc(const void* packed_dev, int input_size, int hidden_size, int num_layers, int output_size,
+                        const void* x, int batch, int seq_len, const int32_t* lengths, const void* h0,
+                        const void* c0, void* out, void* out_seq, void* h_n, void* c_n,
+                        const int32_t* probe_steps, int n_probe, float* probe_h, float* probe_c, void* stream);
+int64_t plh_noalloc_scratch_bytes(void);
+
 /* Synchronise `stream` and read the status word the last plh_forward left in `workspace`
  * (0 = success, else PLH_STATUS_* bits).  Returns PLH_OK or PLH_ERR_HIP. */
 int plh_status(const void* workspace, uint32_t* status, void* stream);

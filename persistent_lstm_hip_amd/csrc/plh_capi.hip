@@ -182,6 +182,30 @@ int device_cus(hipError_t* err) {
   return cus;
 }
 
+// Device scratch of plh_forward_noalloc: one copy on every GPU the library runs on, held until the
+// process ends.  In host code `scratch` names a host-side stand-in, not a device address: host code
+// uses only the per-device address from hipGetSymbolAddress (scratch_ptr).
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::unordered_map<int, void*> g_scratch;
+
+// The device address of `scratch` on the current device, looked up once per device.
+void* scratch_ptr(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch.find(dev);
+  if (it != g_scratch.end()) return it->second;
+  void* ptr = nullptr;
+  *err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (*err != hipSuccess) return nullptr;
+  g_scratch[dev] = ptr;
+  return ptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -410,6 +434,26 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   }
   return PLH_OK;
 }
+
+int plh_forward_noalloc(const void* packed_dev, int input_size, int hidden_size, int num_layers, int output_size,
+                        const void* x, int batch, int seq_len, const int32_t* lengths, const void* h0, const void* c0,
+                        void* out, void* out_seq, void* h_n, void* c_n, const int32_t* probe_steps, int n_probe,
+                        float* probe_h, float* probe_c, void* stream) {
+  const int64_t need = plh_workspace_bytes(input_size, hidden_size, num_layers, output_size, batch, seq_len);
+  if (need < 0) return geometry_code(input_size, hidden_size, num_layers, output_size);
+  if ((uint64_t)need > kScratchBytes)
+    return fail(PLH_ERR_INVALID, "plh_forward_noalloc: this forward needs " + std::to_string(need) +
+                                     " bytes of workspace, more than the " + std::to_string(kScratchBytes >> 20) +
+                                     " MiB of device scratch it holds (use plh_forward with a workspace)");
+  hipError_t err = hipSuccess;
+  void* ws = scratch_ptr(&err);
+  if (!ws) return fail_hip(err, "scratch symbol lookup");
+  return plh_forward(packed_dev, input_size, hidden_size, num_layers, output_size, x, batch, seq_len, lengths, h0, c0,
+                     out, out_seq, h_n, c_n, probe_steps, n_probe, probe_h, probe_c, ws, (int64_t)kScratchBytes,
+                     stream);
+}
+
+int64_t plh_noalloc_scratch_bytes(void) { return (int64_t)kScratchBytes; }
 
 int plh_kernel_timing(int max_forwards) {
   KernelTiming& tm = timing();

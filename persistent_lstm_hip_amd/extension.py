@@ -66,6 +66,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plh_set_wait_limit_us.argtypes = [_i64]
     lib.plh_inject_wait_failure.restype = _i32
     lib.plh_inject_wait_failure.argtypes = [_i32]
+    lib.plh_forward_noalloc.restype = _i32
+    lib.plh_forward_noalloc.argtypes = (
+        [_vp] + [_i32] * 4 + [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp]
+    )
+    lib.plh_noalloc_scratch_bytes.restype = _i64
+    lib.plh_noalloc_scratch_bytes.argtypes = []
     lib.plh_probe_mfma_f16.restype = _i32
     lib.plh_probe_mfma_f16.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
     lib.plh_input_projection.restype = _i32

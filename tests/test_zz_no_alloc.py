@@ -1,0 +1,79 @@
+"""plh_forward_noalloc: the allocation-free variant of plh_forward (device scratch inside the
+library instead of a caller workspace), called through the C ABI.  Checked against plh_forward
+(bit for bit: same kernels, same launch plan) and against the CPU oracle, on two calls in a row, the
+second smaller (it then runs on scratch still holding the first call's data); and its rejection of a
+forward that needs more scratch than it holds."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close, linear_params, make_regressor, make_x, oracle_layers
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+PLH_ERR_INVALID = 1
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _noalloc(gpu, blob, dims, x, probes, outs):
+    I, H, L, O = dims
+    B, T = int(x.size(0)), int(x.size(1))
+    pd = torch.tensor(probes, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    return gpu.lib.plh_forward_noalloc(
+        blob.data_ptr(), I, H, L, O, x.data_ptr(), B, T, None, None, None, outs["out"].data_ptr(),
+        outs["out_seq"].data_ptr(), outs["h_n"].data_ptr(), outs["c_n"].data_ptr(), pd.data_ptr(), len(probes),
+        outs["probe_h"].data_ptr(), outs["probe_c"].data_ptr(), stream)
+
+
+@pytest.mark.parametrize("first,second", [((5, 128, 4, 24, 48, 300), (5, 128, 2, 7, 9, 40)),
+                                          ((5, 256, 2, 6, 40, 64), (3, 100, 3, 5, 5, 17))])
+def test_noalloc_matches_plh_forward_twice(gpu, first, second):
+    assert gpu.lib.plh_noalloc_scratch_bytes() == 64 << 20
+    for I, H, L, O, B, T in (first, second):
+        _say(f"noalloc I={I} H={H} L={L} O={O} B={B} T={T}")
+        native = make_regressor(I, H, L, O)
+        x = make_x(B, T, I)
+        xd = x.to("cuda", torch.float16).contiguous()
+        blob = gpu.pack(*[[getattr(native.lstm, f"{n}_l{l}").detach().cuda() for l in range(L)]
+                          for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")],
+                        native.linear.weight.detach().cuda(), native.linear.bias.detach().cuda())
+        probes = [1, T // 2, T]
+        ref = gpu.forward(blob, (I, H, L, O), xd, want_seq=True, want_state=True, probe_steps=probes,
+                          check_status=True)
+        outs = {k: torch.full_like(v, 7.0) for k, v in ref.items()}
+        rc = _noalloc(gpu, blob, (I, H, L, O), xd, probes, outs)
+        assert rc == 0, gpu.last_error()
+        gpu.check_status(torch.device("cuda"))
+        torch.cuda.synchronize()
+        for k in ref:
+            assert torch.equal(outs[k], ref[k]), f"{k} differs from plh_forward"
+        want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear))
+        assert_close(outs["out"].float().cpu().numpy(), want, what="noalloc head vs oracle")
+
+
+def test_noalloc_rejects_a_forward_larger_than_its_scratch(gpu):
+    _say("noalloc oversize")
+    I, H, L, O, B, T = 5, 128, 4, 24, 512, 1000
+    need = gpu.workspace_bytes(I, H, L, O, B, T)
+    assert need > 64 << 20
+    blob = torch.zeros(gpu.packed_bytes(I, H, L, O), dtype=torch.uint8, device="cuda")
+    x = torch.zeros(B, T, I, dtype=torch.float16, device="cuda")
+    outs = {"out": torch.full((B, O), 7.0, dtype=torch.float16, device="cuda"),
+            "out_seq": torch.full((1,), 7.0, dtype=torch.float16, device="cuda"),
+            "h_n": torch.full((1,), 7.0, dtype=torch.float16, device="cuda"),
+            "c_n": torch.full((1,), 7.0, dtype=torch.float16, device="cuda"),
+            "probe_h": torch.full((1,), 7.0, device="cuda"), "probe_c": torch.full((1,), 7.0, device="cuda")}
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = gpu.lib.plh_forward_noalloc(blob.data_ptr(), I, H, L, O, x.data_ptr(), B, T, None, None, None,
+                                     outs["out"].data_ptr(), None, None, None, None, 0, None, None, stream)
+    assert rc == PLH_ERR_INVALID
+    assert "MiB of device scratch" in gpu.last_error()
+    torch.cuda.synchronize()
+    assert (outs["out"] == 7.0).all(), "nothing may be launched for a rejected forward"

@@ -8,9 +8,12 @@
 //
 //   plh_bench [--input 5] [--hidden 128] [--layers 4] [--output 24] [--batch 512] [--seq 1000]
 //             [--warmup 10] [--iters 100] [--ragged MIN] [--copy-mb N]
+//   plh_bench --gemm K [--cols N] [--batch 512] [--seq 1000] [--blocked 1] [--warmup 10] [--iters 100]
 //
 // --copy-mb N ends the run with three device-to-device copies of N MiB: a plain copy kernel of
 // known size, whose memory counters calibrate the forward's HBM traffic in a profiler.
+// --gemm K times plh_input_projection alone: [batch * seq, K] x [K, N] (N = --cols, default 4 K),
+// fragment-blocked by default (the layer-sequential path's layout), random fp16 operands.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -82,7 +85,59 @@ int arg_int(int argc, char** argv, const char* name, int dflt) {
 
 }  // namespace
 
+// --gemm: the time-parallel input-projection GEMM alone.
+int gemm_main(int argc, char** argv) {
+  const int K = arg_int(argc, argv, "--gemm", 128), N = arg_int(argc, argv, "--cols", 4 * K);
+  const long long M = (long long)arg_int(argc, argv, "--batch", 512) * arg_int(argc, argv, "--seq", 1000);
+  const int blocked = arg_int(argc, argv, "--blocked", 1);
+  const int warmup = arg_int(argc, argv, "--warmup", 10), iters = arg_int(argc, argv, "--iters", 100);
+  const int copy_mb = arg_int(argc, argv, "--copy-mb", 0);
+  Rng rng(7);
+  std::vector<_Float16> w((size_t)N * K);
+  for (auto& e : w) e = (_Float16)(rng.normal() / 16.0);
+  void* d_w = to_device(w.data(), w.size() * 2);
+  std::vector<_Float16> xrow((size_t)1 << 20);
+  for (auto& e : xrow) e = (_Float16)rng.normal();
+  void *d_x = nullptr, *d_c = nullptr;
+  HIP_OK(hipMalloc(&d_x, (size_t)M * K * 2));
+  HIP_OK(hipMalloc(&d_c, (size_t)M * N * 2));
+  for (size_t off = 0; off < (size_t)M * K; off += xrow.size())
+    HIP_OK(hipMemcpy((_Float16*)d_x + off, xrow.data(), std::min(xrow.size(), (size_t)M * K - off) * 2,
+                     hipMemcpyHostToDevice));
+  hipStream_t s;
+  HIP_OK(hipStreamCreate(&s));
+  auto run = [&]() { PLH_OK_(plh_input_projection(d_x, K, d_w, K, d_c, N, M, N, blocked, s)); };
+  for (int i = 0; i < warmup; ++i) run();
+  hipEvent_t e0, e1;
+  HIP_OK(hipEventCreate(&e0));
+  HIP_OK(hipEventCreate(&e1));
+  HIP_OK(hipEventRecord(e0, s));
+  for (int i = 0; i < iters; ++i) run();
+  HIP_OK(hipEventRecord(e1, s));
+  HIP_OK(hipEventSynchronize(e1));
+  float total_ms = 0.f;
+  HIP_OK(hipEventElapsedTime(&total_ms, e0, e1));
+  if (copy_mb > 0) {
+    void *src = nullptr, *dst = nullptr;
+    const size_t bytes = (size_t)copy_mb << 20;
+    HIP_OK(hipMalloc(&src, bytes));
+    HIP_OK(hipMalloc(&dst, bytes));
+    HIP_OK(hipMemsetAsync(src, 1, bytes, s));
+    for (int i = 0; i < 3; ++i) HIP_OK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s));
+    HIP_OK(hipStreamSynchronize(s));
+    HIP_OK(hipFree(src));
+    HIP_OK(hipFree(dst));
+  }
+  const double ms = total_ms / iters, flops = 2.0 * (double)M * N * K;
+  std::printf("{\"gemm\": [%lld, %d, %d], \"blocked\": %d, \"iters\": %d, \"ms\": %.6f, \"tflops\": %.3f}\n", M, K, N,
+              blocked, iters, ms, flops / (ms * 1e-3) / 1e12);
+  std::fflush(stdout);
+  return 0;
+}
+
 int main(int argc, char** argv) {
+  for (int i = 1; i < argc; ++i)
+    if (std::strcmp(argv[i], "--gemm") == 0) return gemm_main(argc, argv);
   const int I = arg_int(argc, argv, "--input", 5), H = arg_int(argc, argv, "--hidden", 128);
   const int L = arg_int(argc, argv, "--layers", 4), O = arg_int(argc, argv, "--output", 24);
   const int B = arg_int(argc, argv, "--batch", 512), T = arg_int(argc, argv, "--seq", 1000);

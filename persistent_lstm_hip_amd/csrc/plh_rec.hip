@@ -10,7 +10,7 @@
 // X0 variant), from x packed in B-fragment order, so nothing of size T x rows x 4H is written.
 //   * the GEMM's output columns are in lane order: W_ih's rows are permuted (and padded to 4 HP) at
 //     pack time so that the 8 projections one lane needs per step (4 gates x 2 units) are 16
-//     contiguous bytes, one load, issued two steps ahead; projections and layer inputs are kept
+//     contiguous bytes, one load, issued a step ahead; projections and layer inputs are kept
 //     fragment-blocked (1 KB per 16 rows x 32 columns), so a wave's projection load and the
 //     GEMM's stores and loads each move one contiguous 1 KB block;
 //   * wave w of a slice holds the i, f, g, o rows of W_hh for unit group w % 4 (16 units) and the
@@ -195,7 +195,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // Input projection of step min(t, Tt - 1) for this lane's row and units, bias excluded: element
   // 2 q + j is gate q of unit eu + j.  Padded units read zero columns and padded rows zero inputs.
   // One unconditional 16-byte load (a load under an exec branch makes the compiler wait for it
-  // together with the ring poll), consumed two steps after it is issued.
+  // together with the ring poll), consumed a step after it is issued.
   // X0: instead, x of step min(t, Tt - 1) as this lane's MFMA B fragment (row en, k 8 kgx .. +7) from
   // xp ([ntile][T][4][16] f16x8).
   // Blocked projections: step t's 16 rows of this tile are block row t * ntile + tile; this lane's
@@ -280,9 +280,12 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
                                      (copy_k8 & 3) * 16 + copy_row;
   auto copy_out = [&](int t, const f16x8& v) { copy_dst[(size_t)t * a.ntile * (HP / 32) * 64] = v; };
   // One step: h_{t-1} in hbuf -> h_t in hbuf; gp holds the input projection of step t (X0: x_t)
-  // and is reloaded with that of step t + 2; gq holds that of step t + 1.  Returns false if a wait
-  // failed.
-  auto step = [&](int t, f16x8& gp, f16x8& gq) -> bool {
+  // on entry and that of step t + 1 on return.  Returns false if a wait failed.
+  // Step t + 1's projection is loaded first: it retires before this step's ring poll (loads retire
+  // in order), about 2000 cycles later, so only stores are in flight when a step ends, on every
+  // path (loop exits included), and the gate math never waits for a load.
+  auto step = [&](int t, f16x8& gp) -> bool {
+    f16x8 gn = gload(t + 1);
     // Partial gate sums of this wave's K half of h_{t-1} (X0: plus x_t W_ih^T of its two gates).
     {
       const f16x8* src = hbuf + e * KCW * FV + lane;
@@ -344,13 +347,16 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // order, so the poll waits for nothing issued after it.
     // Tags of successive writes to a slot (steps t - 2, t) differ, and none is 0 (the cleared ring).
     const uint32_t want = (uint32_t)((t >> 1) % 15) + 1u;
+    // This step's ring slot, uniform by construction: the compiler would otherwise keep its address
+    // in VGPRs (it flows through the lane-conditional store) and put every poll in a waterfall loop.
+    uint64_t* const slot = ring + (size_t)__builtin_amdgcn_readfirstlane(t & 1) * PW;
     {
       const uint32_t mine = enc_half(hcur[0]) | (enc_half(hcur[1]) << 16);
       const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
       const uint64_t tagbits = ((uint64_t)(want & 1u) << 14) | ((uint64_t)((want >> 1) & 1u) << 30) |
                                ((uint64_t)((want >> 2) & 1u) << 46) | ((uint64_t)((want >> 3) & 1u) << 62);
       if ((kgx & 1) == 0)
-        __hip_atomic_store(ring + (size_t)(t & 1) * PW + pwoff, ((uint64_t)mine | ((uint64_t)other << 32)) | tagbits,
+        __hip_atomic_store(slot + pwoff, ((uint64_t)mine | ((uint64_t)other << 32)) | tagbits,
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // The poll reads two adjacent words of a sibling per 16-byte buffer load with cache policy sc1 (what
@@ -362,7 +368,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // different steps, and a load is repeated until both are current).  Half the load
     // instructions of 8-byte atomic loads: C4 21.5 -> 20.0 ms.
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)(t & 1) * PW, 0, PW * 8, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(slot, 0, PW * 8, 0x00020000);
     auto pload = [&](int p) {
       const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (threadIdx.x & 127) * 16u, sib(p) * (PW / 8) * 8, 16);
       wv[2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
@@ -417,10 +423,9 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       for (int p = 0; p < NW / 2; ++p)
         if (p < nld && (ptag(wv[2 * p]) != want || ptag(wv[2 * p + 1]) != want)) pload(p);
     }
-    // gq's load was issued before this step's poll, so it has completed (loads retire in order);
-    // the empty asm tells the compiler, which would otherwise wait for every load in flight at
-    // the next step's gate math.  Then the projection of step t + 2, issued after the poll (the
-    // compiler waits for every load in flight where the poll's retry path joins).
+    // gn's load was issued before this step's poll, so it has completed (loads retire in order);
+    // the empty asm tells the compiler, which would otherwise count the copy below as a read of a
+    // load in flight.
     // Failure injection for tests (plh_inject_wait_failure): workgroup 0 treats this step's wait as
     // timed out; its siblings then find the status word set while they wait for its next words.
     if (t == a.fail_step && blockIdx.x == 0) {
@@ -428,8 +433,8 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       if (threadIdx.x == 0)
         __hip_atomic_fetch_or(a.status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    asm volatile("" : "+v"(gq));
-    gp = gload(t + 2);
+    asm volatile("" : "+v"(gn));
+    gp = gn;
     uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf);
 #pragma unroll
     for (int r = 0; r < NW; ++r)
@@ -442,21 +447,12 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     return __builtin_amdgcn_readfirstlane(s_fail) == 0;
   };
 
-  // Two steps per iteration, so each projection buffer keeps its registers (no copies of loads in
-  // flight, which would wait for them).
-  f16x8 g0 = {}, g1 = {};
-  if (Tt > 0) g0 = gload(0);
-  if (Tt > 1) g1 = gload(1);
-  // Nothing in flight at the loop entry: otherwise the compiler merges a pending g0 into the loop
-  // header and waits for every load at each step's gate math, the one of step t + 1 included.
+  f16x8 gp = {};
+  if (Tt > 0) gp = gload(0);
+  // Nothing in flight at the loop entry, so the first gate math waits for no load.
   wait_vmem_all();
-  // The loop's back edge follows the odd step only: at the top, g0's load has been waited for by
-  // the odd step's poll (loads retire in order), so the gate math waits for nothing in flight.
   bool ok = __builtin_amdgcn_readfirstlane(s_fail) == 0;
-  for (int t = 0; ok && t < Tt; t += 2) {
-    if (!(ok = step(t, g0, g1)) || t + 1 >= Tt) break;
-    if (!(ok = step(t + 1, g1, g0))) break;
-  }
+  for (int t = 0; ok && t < Tt; ++t) ok = step(t, gp);
   // Rows of length 0 keep their h0, which the packed exchange may not carry intact: restore their
   // h in hbuf before it is read as a result (the last copy-out, the head).
   if (ok && a.lengths && Tt > 0) {

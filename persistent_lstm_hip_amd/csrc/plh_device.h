@@ -162,6 +162,40 @@ __device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// XCD-local exchange.  A store without the sc1 bit (a workgroup-scope relaxed atomic store) writes
+// through the CU's L1 into its XCD's L2 and stays there; the exchange's polls (sc1 buffer loads)
+// bypass the reader's L1 and read that L2.  Between CUs of one XCD this hand-off is visible and a
+// round trip costs ~1070 cycles instead of ~1360 for agent-scope stores, which write through to
+// memory (MI355X, one wave per CU); across XCDs such a store is never seen, so it may only be used
+// when every workgroup of the exchange runs on the same XCD.  Tags guard correctness either way: a
+// reader only takes a word whose tag is the current step's.
+__device__ __forceinline__ uint32_t xcc_id() {
+  return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u;  // HW_REG_XCC_ID, bits 3:0
+}
+
+// Thread 0 of each of the n workgroups of an exchange group: publish this XCD's id in table[self]
+// (agent scope; the table is zeroed before the launch) and wait, bounded by wait_ticks, for the
+// other entries.  Returns 1 if all n run on this XCD, 0 if not, -1 if the wait timed out (status
+// set).  Every member sees the same n entries, so all take the same decision.
+__device__ __forceinline__ int same_xcd_group(uint32_t* table, int self, int n, uint32_t* status,
+                                              uint64_t wait_ticks) {
+  const uint32_t mine = xcc_id() + 1u;
+  __hip_atomic_store(table + self, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  int same = 1;
+  for (int s = 0; s < n; ++s) {
+    uint32_t v;
+    while ((v = __hip_atomic_load(table + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0u) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > wait_ticks) {
+        __hip_atomic_fetch_or(status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return -1;
+      }
+    }
+    same &= v == mine;
+  }
+  return same;
+}
+
 // Workgroup -> (layer, tile, slice).  With xcd_map the S slices of a (layer, tile) share an XCD.
 __device__ __forceinline__ void sliced_coords(int b, int ntile, int S, int xcd_map, int& layer, int& tile,
                                               int& slice) {

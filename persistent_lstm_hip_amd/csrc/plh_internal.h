@@ -74,7 +74,8 @@ PackedLayout packed_layout(const Geometry& g);
 // (fragment-blocked: see blocked_index; one 1 KB block per 16 rows x 32 columns)
 //   xp       f16x8 [ntile][T][4][16]               with rec_x0: x in B-fragment order, K zero-padded
 //                                                  to 32 (layer 0's in-kernel projection)
-// and an xring of one layer.
+// and an xring of one layer, followed by u32 [ntile][8]: the XCD id of each slice (+1), zeroed with
+// the ring before each launch.
 struct WorkspaceLayout {
   size_t status, counters, xp, hseq, xring, gates, xs, total;
   size_t xring_words;  // u64 words of xring (0 unless sliced)

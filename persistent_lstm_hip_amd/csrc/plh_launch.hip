@@ -93,7 +93,7 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   if (g.rec) {
     // xp (rec_x0 only) holds x as [ntile][T][4][16] f16x8
     w.hseq = w.xring = align256(w.xp + (g.rec_x0 ? ntile * seq_len * 4 * 16 * 16 : 0));
-    w.xring_words = ntile * 2 * g.HP * 8;
+    w.xring_words = ntile * 2 * g.HP * 8 + ntile * 4;  // the ring, then an 8-entry u32 XCD table per tile
     w.gates = align256(w.xring + w.xring_words * sizeof(uint64_t));
     w.xs = align256(w.gates + (size_t)seq_len * chunk_rows * 4 * g.HP * sizeof(_Float16));
     w.total = align256(w.xs + (size_t)2 * seq_len * chunk_rows * g.HP * sizeof(_Float16));

@@ -21,6 +21,8 @@
 //   * the slices exchange h_t every step through a two-slot ring of tagged 64-bit words, with the
 //     protocol of plh_sliced.hip (readers re-poll words until their tags are current) but packed
 //     words: 4 fp16 and a 4-bit step tag each, and each workgroup polls only its 7 siblings;
+//     when the 8 slices of a tile run on one XCD (checked at entry) the words stay in its L2
+//     (same_xcd_group: ~5850 instead of ~7450 cycles per step at H = 512);
 //     h_t also goes to the next layer's GEMM input, stored a step later from LDS.
 //
 // Reference behaviour restated (mantuoluozk/persistent_lstm_hip): the generic path's per-layer
@@ -107,6 +109,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   __shared__ float2 s_bias[4][HS / 2];
   __shared__ int s_fail;
   __shared__ int s_tlen;
+  __shared__ int s_l2;
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -129,8 +132,19 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // A failed wait of an earlier layer's launch (this forward's status word) fails this one too,
     // so that the head is poisoned whichever layer timed out.
     s_fail = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+    // With xcd_map the 8 slices of a tile are dispatched to one XCD (workgroups go round-robin over
+    // the XCDs, and theirs are congruent mod 8); checked here, and only then do they exchange h
+    // through that XCD's L2 (same_xcd_group; the table follows the ring).
+    s_l2 = 0;
+    if (a.xcd_map) {
+      uint32_t* table = reinterpret_cast<uint32_t*>(a.xring + (size_t)a.ntile * 2 * C::kWords) + tile * S;
+      const int r = same_xcd_group(table, slice, S, a.status, a.wait_ticks);
+      if (r < 0) s_fail = 1;
+      s_l2 = r > 0;
+    }
   }
   __syncthreads();
+  const bool l2 = __builtin_amdgcn_readfirstlane(s_l2) != 0;
   int len = 0;
   if (row_ok) {
     len = a.lengths ? a.lengths[grow] : a.T;
@@ -355,9 +369,13 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
       const uint64_t tagbits = ((uint64_t)(want & 1u) << 14) | ((uint64_t)((want >> 1) & 1u) << 30) |
                                ((uint64_t)((want >> 2) & 1u) << 46) | ((uint64_t)((want >> 3) & 1u) << 62);
-      if ((kgx & 1) == 0)
-        __hip_atomic_store(slot + pwoff, ((uint64_t)mine | ((uint64_t)other << 32)) | tagbits,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint64_t word = ((uint64_t)mine | ((uint64_t)other << 32)) | tagbits;
+      if ((kgx & 1) == 0) {
+        if (l2)
+          __hip_atomic_store(slot + pwoff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else
+          __hip_atomic_store(slot + pwoff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     // The poll reads two adjacent words of a sibling per 16-byte buffer load with cache policy sc1 (what
     // agent-scope relaxed atomics compile to): a descriptor of the ring slot in SGPRs (word 3

@@ -116,15 +116,15 @@ def test_layer_sequential_workspace_layout(ext):
     # layer: 8 workgroups per 16-row tile hold one layer's W_hh, so 256 / 8 = 32 tiles (512 rows) fit
     # one launch.  The workspace holds one layer's input projection for every
     # step (fp16 [T][rows][4HP]), two alternating fp16 layer-input buffers [T][rows][HP], one
-    # layer's exchange ring (tiles * 2 * HP * 8 words of 8 bytes) and, since I <= 32 puts layer 0's
-    # projection inside the recurrent kernel, x as one zero-padded 32-wide MFMA K chunk per row and
-    # step (64 bytes).
+    # layer's exchange ring (tiles * 2 * HP * 8 words of 8 bytes, then 8 u32 per tile) and, since
+    # I <= 32 puts layer 0's projection inside the recurrent kernel, x as one zero-padded 32-wide
+    # MFMA K chunk per row and step (64 bytes).
     L, T, H = 4, 1000, 512
     rows = 512
     b = ext.workspace_bytes(5, H, L, 24, 512, T)
     gates = T * rows * 4 * H * 2
     xs = 2 * T * rows * H * 2
-    ring = (rows // 16) * 2 * H * 8 * 8
+    ring = (rows // 16) * (2 * H * 8 * 8 + 8 * 4)  # + the tile's table of its 8 slices' XCD ids
     xp = rows * T * 64
     assert gates + xs + ring + xp <= b < gates + xs + ring + xp + (1 << 12)
     # I > 32: layer 0's projection is a GEMM too (x goes to the first xs buffer): no packed x

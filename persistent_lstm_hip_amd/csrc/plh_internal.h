@@ -65,7 +65,8 @@ PackedLayout packed_layout(const Geometry& g);
 //                                                  entries of a step's fragment blocks
 //   hseq     f16x8 [L-1][ntile][T][kci][4][R]      h of layers 0..L-2 in B-fragment order
 //   xring    u64 [L][ntile][2][HP * 8]             sliced geometries only: per-step exchange of h
-//                                                  among the slices of a (layer, tile), tagged words
+//                                                  among the slices of a (layer, tile), tagged words;
+//            then u32 [L][ntile][16]               the XCD id (+1) of every slice of a group
 // Layer-sequential geometries (one layer per launch) use instead of xp and hseq:
 //   gates    f16 [T * rows][4 HP] fragment-blocked one layer's input projection x_t W_ih^T, columns
 //                                                  in the recurrent kernel's lane order

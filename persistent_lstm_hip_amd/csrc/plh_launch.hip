@@ -101,7 +101,8 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   }
   w.hseq = align256(w.xp + ntile * seq_len * g.g_in0 * tile_rows * 16);
   w.xring = align256(w.hseq + (size_t)(g.L - 1) * ntile * seq_len * g.kci * frag_bytes);
-  w.xring_words = g.slices > 1 ? (size_t)g.L * ntile * 2 * g.HP * 8 : 0;
+  // the rings, then a u32 table of the slices' XCD ids, up to 16 per (layer, tile)
+  w.xring_words = g.slices > 1 ? (size_t)g.L * ntile * (2 * g.HP * 8 + 8) : 0;
   w.total = align256(w.xring + w.xring_words * sizeof(uint64_t));
   w.gates = w.xs = w.total;
   return w;

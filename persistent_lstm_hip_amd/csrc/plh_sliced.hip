@@ -20,7 +20,8 @@
 // the words themselves until every tag it needs equals t + 1: no store-completion wait, barrier or
 // counter round trip sits between a slice's epilogue and its siblings' next step.  Every word is
 // written and read with agent-scope relaxed 64-bit atomics (sc1), which are single-copy atomic and
-// coherent across the XCDs' L2 caches without cache maintenance.  Two ring slots suffice: a slice
+// coherent across the XCDs' L2 caches without cache maintenance; when all slices of a group run on
+// one XCD (checked at entry) the words are stored without sc1 and stay in its L2 (same_xcd_group).  Two ring slots suffice: a slice
 // can overwrite slot t % 2 with h_{t+2} only after it has read h_{t+1} of every sibling, and a
 // sibling writes h_{t+1} only after it has read h_t from every slice.  The ring is zeroed before
 // each launch (tags start at 1).
@@ -62,6 +63,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   __shared__ int s_ok[2];
   __shared__ int s_fail;
   __shared__ int s_tlen;
+  __shared__ int s_l2;
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -85,8 +87,20 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   if (threadIdx.x == 0) {
     s_tlen = 0;
     s_fail = 0;
+    // With xcd_map the S slices of a (layer, tile group) are dispatched to one XCD; checked here,
+    // and only then do they exchange h through that XCD's L2 (same_xcd_group; the table of the
+    // groups' XCD ids follows the rings).
+    s_l2 = 0;
+    if (a.xcd_map) {
+      uint32_t* table = reinterpret_cast<uint32_t*>(a.xring + (size_t)a.L * a.ntile * 2 * C::kWords) +
+                        ((size_t)layer * (a.ntile / NTI) + tgrp) * S;
+      const int r = same_xcd_group(table, slice, S, a.status, a.wait_ticks);
+      if (r < 0) s_fail = 1;
+      s_l2 = r > 0;
+    }
   }
   __syncthreads();
+  const bool l2 = __builtin_amdgcn_readfirstlane(s_l2) != 0;
 #pragma unroll
   for (int i = 0; i < NTI; ++i) {
     grow[i] = a.row0 + (tgrp * NTI + i) * 16 + en;
@@ -345,11 +359,18 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     if (!active) return;
     const bool live = t < len[i];
     const uint64_t word = tag_word(hcur[i][0], hcur[i][1], (uint32_t)t + 1u);
+    // XCD-local groups store the word without sc1 (it stays in their L2), others with it.
     if constexpr (NTI == 2) {
-      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, word),
-                                            ring_rs(i, t), (uint32_t)woff * 8u, 0, 16);
+      const auto wd = __builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, word);
+      if (l2)
+        __builtin_amdgcn_raw_buffer_store_b64(wd, ring_rs(i, t), (uint32_t)woff * 8u, 0, 1);
+      else
+        __builtin_amdgcn_raw_buffer_store_b64(wd, ring_rs(i, t), (uint32_t)woff * 8u, 0, 16);
     } else {
-      __hip_atomic_store(xr(i) + (size_t)(t & 1) * C::kWords + woff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (l2)
+        __hip_atomic_store(xr(i) + (size_t)(t & 1) * C::kWords + woff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      else
+        __hip_atomic_store(xr(i) + (size_t)(t & 1) * C::kWords + woff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (has_down) {
       union { _Float16 h[2]; uint32_t u; } v;
@@ -402,8 +423,8 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   for (int idx = threadIdx.x; idx < NTI * CH * KCH * FV; idx += NT) ring[idx / (CH * KCH * FV)][idx % (CH * KCH * FV)] = f16x8{};
   __syncthreads();
 
-  bool ok = true;
-  if (Tt > 0) {
+  bool ok = __builtin_amdgcn_readfirstlane(s_fail) == 0;
+  if (ok && Tt > 0) {
     if (has_up) ok = acquire_up(0);
     if (ok) {
       load_chunk(0);

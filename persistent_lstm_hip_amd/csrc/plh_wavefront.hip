@@ -64,27 +64,37 @@ struct Tile {
   static constexpr int kRn = (CH * kKci * kFragVec + kThreads - 1) / kThreads;
 };
 
-// The persistent layer-wavefront recurrence.  Template: padded hidden size HP, batch rows per
-// workgroup ROWS (16, or 8 with the MFMA's B columns 8..15 duplicating rows 0..7 so each lane
-// evaluates two (unit, row) pairs instead of four), steps per hand-off chunk CH, and RAGGED: rows
-// may end before the tile's last step (lengths given); without it every row is live at every step
-// and the state-freezing selects are compiled out.
-template <int HP, int ROWS, int CH, bool RAGGED>
-__global__ void __launch_bounds__(HP / 16 * 64)
-lstm_wavefront_kernel(ForwardArgs a) {
+// LDS of one workgroup.  Ring and history are double-buffered by chunk parity, so chunk k+1's
+// inputs can be written and chunk k-1's h copied out while chunk k runs.
+template <int HP, int ROWS, int CH>
+struct WavefrontLds {
+  using C = Tile<HP, ROWS, CH>;
+  f16x8 ring[2 * CH * C::kKci * C::kFragVec];  // step inputs: chunk k in buffer k & 1
+  f16x8 hist[2 * CH * C::kKcr * C::kFragVec];  // h of every step: step (k, s) in buffer k & 1, slot s
+  int ok;
+  int tlen;
+};
+
+// The persistent layer-wavefront recurrence of one (layer, tile).  Template: padded hidden size HP,
+// batch rows per workgroup ROWS (16, or 8 with the MFMA's B columns 8..15 duplicating rows 0..7 so
+// each lane evaluates two (unit, row) pairs instead of four), steps per hand-off chunk CH, RAGGED:
+// rows may end before the tile's last step (lengths given; without it every row is live at every
+// step and the state-freezing selects are compiled out), and IN0: the input part is a single K
+// chunk (layer 0 with I <= 32), so the input MFMAs on the other, all-zero chunks are skipped.
+template <int HP, int ROWS, int CH, bool RAGGED, bool IN0>
+__device__ __forceinline__ void wavefront_body(const ForwardArgs& a, WavefrontLds<HP, ROWS, CH>& lds, int layer,
+                                               int tile) {
   using C = Tile<HP, ROWS, CH>;
   constexpr int KCI = C::kKci, KCR = C::kKcr, KC = C::kKc, NT = C::kThreads, FV = C::kFragVec;
+  constexpr int KIN = IN0 ? 1 : KCI;  // input-part K chunks with MFMA work
   constexpr int UPL = C::kUpl, RN = C::kRn;
   static_assert(CH >= 4 && (CH & (CH - 1)) == 0, "the hand-off schedule needs a power-of-two chunk of >= 4 steps");
   constexpr int kRingBuf = CH * KCI * FV;  // f16x8 per ring buffer (one chunk of step inputs)
   constexpr int kHistBuf = CH * KCR * FV;  // f16x8 per history buffer (one chunk of h)
-
-  // Both are double-buffered by chunk parity, so chunk k+1's inputs can be written and chunk k-1's
-  // h copied out while chunk k runs.
-  __shared__ f16x8 ring[2 * kRingBuf];  // step inputs: chunk k in buffer k & 1
-  __shared__ f16x8 hist[2 * kHistBuf];  // h of every step: step (k, s) in buffer k & 1, slot s
-  __shared__ int s_ok;
-  __shared__ int s_tlen;
+  f16x8* const ring = lds.ring;
+  f16x8* const hist = lds.hist;
+  int& s_ok = lds.ok;
+  int& s_tlen = lds.tlen;
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -92,8 +102,6 @@ lstm_wavefront_kernel(ForwardArgs a) {
   const int kg = lane >> 4;           // K group of the A/B fragments, row group of D
   const int r = n & (ROWS - 1);       // batch row in the tile
   const int fl = kg * ROWS + r;       // this lane's B fragment within a block
-  int layer, tile;
-  block_coords(blockIdx.x, a.ntile, a.xcd_map, layer, tile);
 
   const int grow = a.row0 + tile * ROWS + r;
   const bool row_ok = grow < a.row_end;
@@ -115,7 +123,7 @@ lstm_wavefront_kernel(ForwardArgs a) {
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
+      for (int q = 0; q < 4; ++q) w[kc][q] = (kc < KIN || kc >= KCI) ? wp[(kc * 4 + q) * 64] : f16x8{};
   }
   // D rows of this lane: units u0 .. u0+3 of row n; it evaluates UPL of them, starting at uo.
   const int u0 = wave * 16 + kg * 4;
@@ -250,13 +258,13 @@ lstm_wavefront_kernel(ForwardArgs a) {
   f32x4 acc_next[4];
   if (ok && Tt > 0) {
     const f16x8* xr = ring + fl;
-    f16x8 xv[KCI];
+    f16x8 xv[KIN];
 #pragma unroll
-    for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
+    for (int kc = 0; kc < KIN; ++kc) xv[kc] = xr[kc * FV];
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
 #pragma unroll
-    for (int kc = 0; kc < KCI; ++kc)
+    for (int kc = 0; kc < KIN; ++kc)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         acc_next[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], xv[kc], acc_next[q], 0, 0, 0);
@@ -299,9 +307,9 @@ lstm_wavefront_kernel(ForwardArgs a) {
     // (in-order issue would otherwise queue all VALU work behind a burst of MFMAs).
     const int tn = min(t + 1, Tt - 1);
     const f16x8* xr = ring + ((tn / CH) & 1) * kRingBuf + (tn % CH) * (KCI * FV) + fl;
-    f16x8 xv[KCI];
+    f16x8 xv[KIN];
 #pragma unroll
-    for (int kc = 0; kc < KCI; ++kc) xv[kc] = xr[kc * FV];
+    for (int kc = 0; kc < KIN; ++kc) xv[kc] = xr[kc * FV];
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc_next[q] = bias[q];
     const bool live = t < len;
@@ -331,22 +339,22 @@ lstm_wavefront_kernel(ForwardArgs a) {
       // queues its gate math behind a burst of MFMAs.
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int m = 0; m < KCI * 4; ++m) input_mfma(m);
+      for (int m = 0; m < KIN * 4; ++m) input_mfma(m);
 #pragma unroll
       for (int j = 0; j < UPL; ++j) cell_pair(j);
 #pragma unroll
-      for (int m = 0; m < KCI * 4; ++m) {
+      for (int m = 0; m < KIN * 4; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
       }
       __builtin_amdgcn_sched_barrier(0);
     } else {
       // Four pairs per lane: each pair is preceded by its share of the MFMAs and fenced.
-      constexpr int kMfmaPerPiece = (KCI * 4 + UPL - 1) / UPL;
+      constexpr int kMfmaPerPiece = (KIN * 4 + UPL - 1) / UPL;
 #pragma unroll
       for (int j = 0; j < UPL; ++j) {
 #pragma unroll
-        for (int m = j * kMfmaPerPiece; m < (j + 1) * kMfmaPerPiece && m < KCI * 4; ++m) input_mfma(m);
+        for (int m = j * kMfmaPerPiece; m < (j + 1) * kMfmaPerPiece && m < KIN * 4; ++m) input_mfma(m);
         cell_pair(j);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -465,6 +473,21 @@ lstm_wavefront_kernel(ForwardArgs a) {
       a.out[(size_t)g * a.O + o] = (_Float16)(a.blin[o] + (s0 + s1));
     }
   }
+}
+
+
+// One workgroup per (layer, tile).  Layer 0 with x inside one 32-wide K chunk (I <= 32: at most 4
+// 8-wide K groups) takes the IN0 body, chosen once here, so no step of either body branches on it.
+template <int HP, int ROWS, int CH, bool RAGGED>
+__global__ void __launch_bounds__(HP / 16 * 64)
+lstm_wavefront_kernel(ForwardArgs a) {
+  __shared__ WavefrontLds<HP, ROWS, CH> lds;
+  int layer, tile;
+  block_coords(blockIdx.x, a.ntile, a.xcd_map, layer, tile);
+  if (layer == 0 && a.g_in0 <= 4)
+    wavefront_body<HP, ROWS, CH, RAGGED, true>(a, lds, layer, tile);
+  else
+    wavefront_body<HP, ROWS, CH, RAGGED, false>(a, lds, layer, tile);
 }
 
 }  // namespace

@@ -4,7 +4,7 @@
 //
 // X is a layer's input sequence for every (step, row) of a launch ([T * rows][ldx], K-contiguous),
 // W is that layer's W_ih ([N = 4 HP][K], K-contiguous, rows in the recurrent kernel's lane order),
-// C the gate pre-activations the recurrent kernel reads two steps ahead.  It restates the
+// C the gate pre-activations the recurrent kernel reads a step ahead.  It restates the
 // reference's per-layer torch::matmul of fp16 tensors (persistent_lstm_hip.cu:2988-2994, fp16
 // result), written as a hand-written MFMA kernel instead of a library GEMM.
 //

@@ -350,9 +350,9 @@ def test_layer_sequential_path_dropin_with_state_and_ragged(gpu, H):
 
 @pytest.mark.parametrize("T", [1, 2, 3])
 def test_layer_sequential_short_sequences(gpu, T):
-    """Layer-sequential path with 1, 2 and 3 steps (the kernel runs two steps per loop iteration and
-    loads the projection two steps ahead, clamped to the last step): 600 rows are a 512-row launch
-    and an 88-row one (6 tiles, no XCD mapping).  Full output sequence and final state vs torch fp32."""
+    """Layer-sequential path with 1, 2 and 3 steps (the kernel loads each step's projection a step
+    ahead, clamped to the last step): 600 rows are a 512-row launch and an 88-row one (6 tiles, no
+    XCD mapping, so agent-scope exchange).  Full output sequence and final state vs torch fp32."""
     I, H, L, B = 5, 512, 2, 600
     _say(f"layer-sequential short T={T}")
     torch.manual_seed(41)

@@ -76,15 +76,16 @@ __device__ __attribute__((unused)) int wait_counter(const uint32_t* ctr, uint32_
   return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
 }
 
-// After a failed wait: NaN into every output element a lane owns, units u0 .. u0 + n - 1 of batch row
-// `grow` in `layer`: h_n, c_n, every probe and, for the last layer, every step of out_seq.  With the
-// head poisoned as well, each output element of a forward is then either its correct value or NaN.
+// After a failed wait: NaN into every output element a lane owns, units u0 + stride * j (j < n) of
+// batch row `grow` in `layer`: h_n, c_n, every probe and, for the last layer, every step of out_seq.
+// With the head poisoned as well, each output element of a forward is then either its correct value
+// or NaN.
 __device__ __attribute__((unused)) void poison_lane_outputs(const ForwardArgs& a, int layer, int grow, int u0, int n,
-                                                            bool last) {
+                                                            bool last, int stride = 1) {
   const float qnan = __builtin_nanf("");
   const _Float16 hnan = (_Float16)qnan;
   for (int j = 0; j < n; ++j) {
-    const int u = u0 + j;
+    const int u = u0 + stride * j;
     if (u >= a.H) continue;
     const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
     if (a.h_n) a.h_n[si] = hnan;
@@ -133,14 +134,13 @@ struct Sliced {
 
 // Work split of the layer-sequential recurrent kernel (padded H = 512, plh_rec.hip): the input
 // projection comes precomputed, so a workgroup holds only W_hh rows, for HS = 64 hidden units, and
-// S = 8 workgroups serve a 16-row tile.  Wave w serves unit group w % 4 (16 units) with the K half
-// w / 4 of h_{t-1} (8 K-chunks of 32 x 4 gates = 128 VGPRs).
+// S = 8 workgroups serve a 16-row tile.  Wave w serves units 8 w .. 8 w + 7 of the slice over all
+// of K (16 K-chunks of 32 x 2 tiles of 16 gate rows = 128 VGPRs).
 template <int HP>
 struct Rec {
   static constexpr int kS = 8;            // workgroups per 16-row tile
   static constexpr int kHs = HP / kS;     // hidden units per workgroup
   static constexpr int kKch = HP / 32;    // K chunks of h
-  static constexpr int kKcw = kKch / 2;   // K chunks per wave
   static constexpr int kWords = HP * 8;   // ring words reserved per step slot of a tile (the packed
                                           // words of one step take half)
   static_assert(kHs == 64, "four 16-unit groups per workgroup");

@@ -13,11 +13,14 @@
 //     contiguous bytes, one load, issued a step ahead; projections and layer inputs are kept
 //     fragment-blocked (1 KB per 16 rows x 32 columns), so a wave's projection load and the
 //     GEMM's stores and loads each move one contiguous 1 KB block;
-//   * wave w of a slice holds the i, f, g, o rows of W_hh for unit group w % 4 (16 units) and the
-//     K half w / 4 of h_{t-1}: 8 K-chunks x 4 gates of MFMA A fragments (128 VGPRs);
-//   * per step each wave computes its partial gate sums from h_{t-1} in LDS (32 MFMAs), the two
-//     K halves meet in LDS, and the two waves of a group split its 16 units x 16 rows (two units
-//     per lane), adding the bias and the precomputed input projection;
+//   * wave w of a slice holds the i, f, g, o rows of W_hh for its 8 units (8 w .. 8 w + 7) over all
+//     of K, as two 16-row tiles whose rows interleave the gates (row r: gate r % 4 of unit
+//     4 j + r / 4): 16 K-chunks x 2 tiles of MFMA A fragments (128 VGPRs);
+//   * per step each wave computes its gate sums from h_{t-1} in LDS (32 MFMAs, two independent
+//     chains) and each lane then holds all four gates of units (eu, eu + 4) for one row, so the
+//     cell update needs no other wave: no partial sums and no barrier between a wave's MFMAs and
+//     its gate math, and one wave of a SIMD updates its cells while the other still runs its
+//     MFMAs.  h is double-buffered in LDS by step;
 //   * the slices exchange h_t every step through a two-slot ring of tagged 64-bit words, with the
 //     protocol of plh_sliced.hip (readers re-poll words until their tags are current) but packed
 //     words: 4 fp16 and a 4-bit step tag each, and each workgroup polls only its 7 siblings;
@@ -33,27 +36,32 @@
 namespace plh {
 namespace {
 
-// [L][S][8 waves][8 chunks][4 gates][64 lanes][8]: wave w of slice s holds W_hh rows of unit group
-// w % 4 and K half w / 4.
+// [L][S][8 waves][16 chunks][2 tiles][64 lanes][8]: wave w of slice s holds the W_hh rows of its 8
+// units s * 64 + 8 w .. + 7 for all of K; row r of tile j's A fragment is gate r % 4 of unit
+// s * 64 + 8 w + 4 j + r / 4, so the D fragment of tile j gives lane l all four gates of unit
+// s * 64 + 8 w + 4 j + l / 16 for batch row l % 16.
 template <int HP>
 __global__ void pack_rec_kernel(const _Float16* __restrict__ w_hh, int H, _Float16* __restrict__ dst) {
   using C = Rec<HP>;
-  const size_t total = (size_t)C::kS * 8 * C::kKcw * 4 * 64 * 8;
+  const size_t total = (size_t)C::kS * 8 * C::kKch * 2 * 64 * 8;
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= total) return;
-  const int j = e & 7;
+  const int jj = e & 7;
   const int lane = (e >> 3) & 63;
-  const int q = (e >> 9) & 3;
-  const int kc = (int)((e >> 11) & 7);
-  const int wv = (int)((e >> 14) & 7);
-  const int sl = (int)(e >> 17);
-  const int u = sl * C::kHs + (wv & 3) * 16 + (lane & 15);
-  const int k = ((wv >> 2) * C::kKcw + kc) * 32 + (lane >> 4) * 8 + j;
+  const int j = (e >> 9) & 1;
+  const int kc = (int)((e >> 10) % C::kKch);
+  const size_t wsl = (e >> 10) / C::kKch;
+  const int wv = (int)(wsl & 7);
+  const int sl = (int)(wsl >> 3);
+  const int r = lane & 15;
+  const int u = sl * C::kHs + wv * 8 + 4 * j + (r >> 2);
+  const int q = r & 3;
+  const int k = kc * 32 + (lane >> 4) * 8 + jj;
   dst[e] = (u < H && k < H) ? w_hh[((size_t)q * H + u) * H + k] : (_Float16)0.0f;
 }
 
 // Column of the input projection that lane `lane` of wave `wave` in slice `slice` reads as element
-// 2 q + j: gate q of unit slice * 64 + (wave % 4) * 16 + (lane / 16) * 4 + 2 (wave / 4) + j.
+// 2 q + j: gate q of unit slice * 64 + 8 wave + lane / 16 + 4 j.
 __host__ __device__ constexpr int rec_gate_col(int slice, int wave, int kgx) {
   return ((slice * 8 + wave) * 4 + kgx) * 8;
 }
@@ -66,19 +74,19 @@ __global__ void pack_rec_wih_kernel(const _Float16* __restrict__ w_ih, int H, in
   if (e >= (size_t)4 * HP * Kp) return;
   const int col = (int)(e / Kp), k = (int)(e % Kp);
   const int q = (col & 7) >> 1, j = col & 1, kgx = (col >> 3) & 3, wave = (col >> 5) & 7, slice = col >> 8;
-  const int u = slice * 64 + (wave & 3) * 16 + kgx * 4 + 2 * (wave >> 2) + j;
+  const int u = slice * 64 + wave * 8 + kgx + 4 * j;
   dst[e] = (u < H && k < K) ? w_ih[((size_t)q * H + u) * K + k] : (_Float16)0.0f;
 }
 
-// W_ih of layer 0 (I <= 32) as MFMA A fragments of the X0 kernel: [8 slices][8 waves][2][64 lanes][8];
-// wave w holds gates 2 (w / 4) and 2 (w / 4) + 1 of unit group w % 4 (lane l: unit row l % 16, k =
-// 8 (l / 16) + 0..7), so the two K-half waves of a group share the four gates.
+// W_ih of layer 0 (I <= 32) as MFMA A fragments of the X0 kernel: [8 slices][8 waves][2 tiles][64 lanes][8],
+// tile j's rows as in pack_rec_kernel (gate r % 4 of unit 8 w + 4 j + r / 4) and k = 8 (l / 16) + 0..7.
 __global__ void pack_rec_wx0_kernel(const _Float16* __restrict__ w_ih, int H, int I, _Float16* __restrict__ dst) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (size_t)Rec<512>::kS * 8 * 2 * 64 * 8) return;
   const int jj = e & 7, lane = (e >> 3) & 63, j = (e >> 9) & 1, wv = (e >> 10) & 7, sl = (int)(e >> 13);
-  const int u = sl * Rec<512>::kHs + (wv & 3) * 16 + (lane & 15);
-  const int q = 2 * (wv >> 2) + j, k = (lane >> 4) * 8 + jj;
+  const int r = lane & 15;
+  const int u = sl * Rec<512>::kHs + wv * 8 + 4 * j + (r >> 2);
+  const int q = r & 3, k = (lane >> 4) * 8 + jj;
   dst[e] = (u < H && k < I) ? w_ih[((size_t)q * H + u) * I + k] : (_Float16)0.0f;
 }
 
@@ -100,13 +108,15 @@ __global__ void rec_input_kernel(const _Float16* __restrict__ x, int T, int I, i
 template <int HP, bool X0>
 __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   using C = Rec<HP>;
-  constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch, KCW = C::kKcw;
+  constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch;
   constexpr int NT = 512, FV = 64, NW = 4;  // packed words each thread gathers per step (at most)
   constexpr int PW = C::kWords / 2;          // packed words of one step's h of a tile (4 fp16 each)
 
-  __shared__ f16x8 hbuf[KCH * FV];  // h_{t-1} of all HP units, fragment order
-  __shared__ f32x4 part[8][4][64];  // partial gate sums of every wave
-  __shared__ float2 s_bias[4][HS / 2];
+  // h of all HP units in fragment order, double-buffered by step: step t reads h_{t-1} from buffer
+  // t & 1 and writes h_t (its own units and the gathered ones) into the other, so no wave waits for
+  // the others between its MFMAs and its gate math.
+  __shared__ f16x8 hbuf[2][KCH * FV];
+  __shared__ float s_bias[4][HS];
   __shared__ int s_fail;
   __shared__ int s_tlen;
   __shared__ int s_l2;
@@ -116,12 +126,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   int unused_layer, tile, slice;
   sliced_coords(blockIdx.x, a.ntile, S, a.xcd_map, unused_layer, tile, slice);
   const int layer = a.layer;
-  const int g = wave & 3, e = wave >> 2;  // unit group, K half
-  const bool e0 = __builtin_amdgcn_readfirstlane(e) == 0;
   const int en = lane & 15, kgx = lane >> 4;
-  // This lane's units eu, eu + 1 of row en: elements 2e, 2e + 1 of lane `lane` of the group's D
-  // fragments (units 4 kgx + i, row en).
-  const int eu = slice * HS + g * 16 + kgx * 4 + 2 * e;
+  // This lane's units eu and eu + 4 of row en: the D fragments of the wave's two tiles (all four
+  // gates of unit 8 wave + 4 j + kgx of the slice, row en).
+  const int eu = slice * HS + wave * 8 + kgx;
   const int b = tile * 16 + en;  // row within this launch
   const int grow = a.row0 + b;
   const bool row_ok = grow < a.row_end;
@@ -156,16 +164,16 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // readfirstlane, so that the loop's exits are uniform branches the compiler leaves unstructured.
   const int Tt = __builtin_amdgcn_readfirstlane(s_tlen);
 
-  f16x8 w[KCW][4];
+  f16x8 w[KCH][2];
   {
     const f16x8* wp =
-        reinterpret_cast<const f16x8*>(a.wpack) + (size_t)((layer * S + slice) * 8 + wave) * KCW * 4 * 64 + lane;
+        reinterpret_cast<const f16x8*>(a.wpack) + (size_t)((layer * S + slice) * 8 + wave) * KCH * 2 * 64 + lane;
 #pragma unroll
-    for (int kc = 0; kc < KCW; ++kc)
+    for (int kc = 0; kc < KCH; ++kc)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
+      for (int j = 0; j < 2; ++j) w[kc][j] = wp[(kc * 2 + j) * 64];
   }
-  // X0: W_ih of layer 0 for gates 2e, 2e + 1 of this wave's unit group.
+  // X0: W_ih of layer 0 for the wave's two tiles.
   f16x8 wx[2] = {};
   if constexpr (X0) {
     const f16x8* p = reinterpret_cast<const f16x8*>(a.wx0) + (size_t)(slice * 8 + wave) * 2 * 64 + lane;
@@ -175,17 +183,16 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // The resident weights complete here (otherwise the compiler keeps them "possibly outstanding"
   // and waits for every global access in flight before the step loop's MFMAs).
   __builtin_amdgcn_s_waitcnt(0);
-  for (int idx = threadIdx.x; idx < 4 * HS / 2; idx += NT) {
-    const int q = idx / (HS / 2), up = idx % (HS / 2);
-    const float* bp = a.bias + ((size_t)layer * 4 + q) * HP + slice * HS + 2 * up;
-    s_bias[q][up] = float2{bp[0], bp[1]};
+  for (int idx = threadIdx.x; idx < 4 * HS; idx += NT) {
+    const int q = idx / HS, u = idx % HS;
+    s_bias[q][u] = a.bias[((size_t)layer * 4 + q) * HP + slice * HS + u];
   }
 
   float c[2];
   _Float16 hcur[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int u = eu + j;
+    const int u = eu + 4 * j;
     const bool v = row_ok && u < a.H;
     const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
     c[j] = (v && a.c0) ? (float)a.c0[si] : 0.0f;
@@ -202,12 +209,12 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       for (int j = 0; j < 8; ++j)
         if (k0 + j < a.H) v[j] = a.h0[((size_t)layer * a.B + gr) * a.H + k0 + j];
     }
-    hbuf[idx] = v;
+    hbuf[0][idx] = v;
   }
   __syncthreads();  // hbuf and s_bias complete before the first step (or the head, if no step runs)
 
   // Input projection of step min(t, Tt - 1) for this lane's row and units, bias excluded: element
-  // 2 q + j is gate q of unit eu + j.  Padded units read zero columns and padded rows zero inputs.
+  // 2 q + j is gate q of unit eu + 4 j.  Padded units read zero columns and padded rows zero inputs.
   // One unconditional 16-byte load (a load under an exec branch makes the compiler wait for it
   // together with the ring poll), consumed a step after it is issued.
   // X0: instead, x of step min(t, Tt - 1) as this lane's MFMA B fragment (row en, k 8 kgx .. +7) from
@@ -224,9 +231,9 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     return gsrc[tc * a.ntile * (4 * HP / 32) * 64];
   };
 
-  // Packed exchange.  A word carries 4 fp16 of one row: the pair of a lane with even kgx (units
-  // 4 kgx + 2e, +1) and that of its partner lane + 16 (the next 4 units), and a 4-bit step tag in
-  // bit 14 of each fp16.  That bit is clear in every h a step computes (|h| <= 1 < 2); NaN and
+  // Packed exchange.  A word carries 4 fp16 of one row: units eu, eu + 1 (low half) and eu + 4,
+  // eu + 5 (high half) of a lane with even kgx, which holds eu and eu + 4 and takes eu + 1 and eu + 5
+  // from its partner lane + 16, and a 4-bit step tag in bit 14 of each fp16.  That bit is clear in every h a step computes (|h| <= 1 < 2); NaN and
   // infinity, the only other values with it set, travel as +-1.5 (never an h) and come back as NaN.
   // The bit is cleared in every value sent, so the tag is always intact; rows of length 0 keep their
   // h0, which may use it: their exchanged values only feed their own (frozen) rows and are restored
@@ -248,10 +255,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   auto gdst = [&](int r) -> int {
     const int wq = 2 * (threadIdx.x & 127) + (r & 1);  // word within the sibling's block
     const int wv_ = wq >> 5, en_ = wq & 15, kgx_ = 2 * ((wq >> 4) & 1);
-    const int eu_ = sib(r >> 1) * HS + (wv_ & 3) * 16 + kgx_ * 4 + 2 * (wv_ >> 2);
+    const int eu_ = sib(r >> 1) * HS + wv_ * 8 + kgx_;
     return ((eu_ >> 3) * 16 + en_) * 4 + ((eu_ & 7) >> 1);
   };
-  const int own_dst = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's pair in hbuf
+  const int own_dst = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's word's first pair in hbuf (even kgx)
   auto enc_half = [](_Float16 h) -> uint32_t {
     const uint32_t b = __builtin_bit_cast(uint16_t, h);
     return (b & 0x7C00u) == 0x7C00u ? (b & 0x8000u) | 0x3E00u : b & 0xBFFFu;
@@ -266,6 +273,13 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     return (uint32_t)(((w >> 14) & 1u) | ((w >> 29) & 2u) | ((w >> 44) & 4u) | ((w >> 59) & 8u));
   };
 
+  // b_ih + b_hh of this lane's units (eu + 4 j) by gate, in registers for the whole sequence.
+  float bias[4][2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bias[q][j] = s_bias[q][wave * 8 + kgx + 4 * j];
+
   int probe_i = 0;
   // Probe steps live in SGPRs (a VGPR loaded in the loop would put a vmcnt(0) on every step).
   int probe_next = a.n_probe > 0 ? __builtin_amdgcn_readfirstlane(a.probe_steps[0]) : -1;
@@ -273,7 +287,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     if (!row_ok) return;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int u = eu + j;
+      const int u = eu + 4 * j;
       if (u < a.H) {
         const size_t o = (((size_t)pi * a.L + layer) * a.B + grow) * a.H + u;
         a.probe_h[o] = (float)hcur[j];
@@ -293,65 +307,59 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
                                : reinterpret_cast<f16x8*>(a.hout) + ((size_t)tile * (HP / 32) + (copy_k8 >> 2)) * 64 +
                                      (copy_k8 & 3) * 16 + copy_row;
   auto copy_out = [&](int t, const f16x8& v) { copy_dst[(size_t)t * a.ntile * (HP / 32) * 64] = v; };
-  // One step: h_{t-1} in hbuf -> h_t in hbuf; gp holds the input projection of step t (X0: x_t)
-  // on entry and that of step t + 1 on return.  Returns false if a wait failed.
+  // One step: h_{t-1} in hbuf[t & 1] -> h_t in hbuf[(t + 1) & 1]; gp holds the input projection of
+  // step t (X0: x_t) on entry and that of step t + 1 on return.  Returns false if a wait failed.
   // Step t + 1's projection is loaded first: it retires before this step's ring poll (loads retire
   // in order), about 2000 cycles later, so only stores are in flight when a step ends, on every
   // path (loop exits included), and the gate math never waits for a load.
   auto step = [&](int t, f16x8& gp) -> bool {
     f16x8 gn = gload(t + 1);
-    // Partial gate sums of this wave's K half of h_{t-1} (X0: plus x_t W_ih^T of its two gates).
-    {
-      const f16x8* src = hbuf + e * KCW * FV + lane;
-      f32x4 acc[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (X0) {
-        if (e0) {
-          acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[0], gp, acc[0], 0, 0, 0);
-          acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[1], gp, acc[1], 0, 0, 0);
-        } else {
-          acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[0], gp, acc[2], 0, 0, 0);
-          acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[1], gp, acc[3], 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int kc = 0; kc < KCW; ++kc) {
-        const f16x8 bv = src[kc * FV];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], bv, acc[q], 0, 0, 0);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) part[wave][q][lane] = acc[q];
+    const f16x8* const hprev = hbuf[t & 1];
+    f16x8* const hnext = hbuf[(t + 1) & 1];
+    // The gate sums of the wave's two tiles over all of K (X0: plus x_t W_ih^T), two independent
+    // MFMA chains fed by one 16-byte LDS read per K chunk.
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    if constexpr (X0) {
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[0], gp, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[1], gp, acc[1], 0, 0, 0);
     }
-    // h_{t-1} of this slice's units, 16 bytes per thread of waves 0-1, read before the barrier
-    // after which the step's gather overwrites hbuf; stored below as the next layer's input.
+    // The h fragments are read from LDS four K-chunks ahead of their MFMAs (one read in flight
+    // per chunk would leave the matrix core waiting for LDS latency at every chunk).
+    constexpr int kAhead = 4;
+    f16x8 bq[kAhead];
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) bq[i] = hprev[i * FV + lane];
+#pragma unroll
+    for (int kc = 0; kc < KCH; ++kc) {
+      const f16x8 bv = bq[kc % kAhead];
+      if (kc + kAhead < KCH) bq[kc % kAhead] = hprev[(kc + kAhead) * FV + lane];
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][0], bv, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][1], bv, acc[1], 0, 0, 0);
+    }
+    // h_{t-1} of this slice's units, 16 bytes per thread of waves 0-1, stored below as the next
+    // layer's input (hbuf[t & 1] is overwritten only in step t + 1).
     f16x8 hcp = {};
-    if (!last && threadIdx.x < kCopyThreads) hcp = hbuf[copy_src];
-    lds_barrier();
+    if (!last && threadIdx.x < kCopyThreads) hcp = hprev[copy_src];
 
-    // Gate math: bias + both K halves + the input projection.
+    // Gate math on the accumulators: element q of tile j is gate q of unit eu + 4 j.
     const bool live = t < len;
     {
       float z[4][2];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float2 bv = s_bias[q][(eu - slice * HS) >> 1];
-        z[q][0] = X0 ? bv.x : bv.x + (float)gp[2 * q];
-        z[q][1] = X0 ? bv.y : bv.y + (float)gp[2 * q + 1];
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int ee = 0; ee < 2; ++ee) {
-          const float2 v = reinterpret_cast<const float2*>(&part[ee * 4 + g][q][lane])[e];
-          z[q][0] += v.x;
-          z[q][1] += v.y;
-        }
-      }
+        for (int j = 0; j < 2; ++j)
+          z[q][j] = X0 ? acc[j][q] + bias[q][j] : acc[j][q] + bias[q][j] + (float)gp[2 * q + j];
+      float cn[2] = {c[0], c[1]}, hn[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn[j], hn[j]);
+      // Both units' updates are computed on every lane and then selected: otherwise the compiler
+      // puts each behind a branch on `live`, which serialises the two units' dependency chains.
+      asm volatile("" : "+v"(cn[0]), "+v"(cn[1]), "+v"(hn[0]), "+v"(hn[1]));
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        float cn = c[j], hn;
-        lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn, hn);
-        c[j] = live ? cn : c[j];
-        hcur[j] = live ? (_Float16)hn : hcur[j];
+        c[j] = live ? cn[j] : c[j];
+        hcur[j] = live ? (_Float16)hn[j] : hcur[j];
       }
     }
 
@@ -364,12 +372,17 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // This step's ring slot, uniform by construction: the compiler would otherwise keep its address
     // in VGPRs (it flows through the lane-conditional store) and put every poll in a waterfall loop.
     uint64_t* const slot = ring + (size_t)__builtin_amdgcn_readfirstlane(t & 1) * PW;
+    // The word's pairs (eu, eu + 1) and (eu + 4, eu + 5): this lane holds eu and eu + 4, its
+    // partner lane + 16 (kgx + 1) eu + 1 and eu + 5.
+    uint32_t pair_lo, pair_hi;
     {
       const uint32_t mine = enc_half(hcur[0]) | (enc_half(hcur[1]) << 16);
       const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
+      pair_lo = __builtin_amdgcn_perm(other, mine, 0x05040100u);
+      pair_hi = __builtin_amdgcn_perm(other, mine, 0x07060302u);
       const uint64_t tagbits = ((uint64_t)(want & 1u) << 14) | ((uint64_t)((want >> 1) & 1u) << 30) |
                                ((uint64_t)((want >> 2) & 1u) << 46) | ((uint64_t)((want >> 3) & 1u) << 62);
-      const uint64_t word = ((uint64_t)mine | ((uint64_t)other << 32)) | tagbits;
+      const uint64_t word = ((uint64_t)pair_lo | ((uint64_t)pair_hi << 32)) | tagbits;
       if ((kgx & 1) == 0) {
         if (l2)
           __hip_atomic_store(slot + pwoff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -395,12 +408,12 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
 #pragma unroll
     for (int p = 0; p < NW / 2; ++p)
       if (p < nld) pload(p);
-    // This lane's own pair of h_t (no step-t reader of hbuf is left after the first barrier).
-    {
-      union { _Float16 h[2]; uint32_t u; } v;
-      v.h[0] = hcur[0];
-      v.h[1] = hcur[1];
-      reinterpret_cast<uint32_t*>(hbuf)[own_dst] = v.u;
+    // This slice's own pairs of h_t, from the lanes that send them (nobody reads hbuf[(t + 1) & 1]
+    // in step t).
+    if ((kgx & 1) == 0) {
+      uint32_t* own32 = reinterpret_cast<uint32_t*>(hnext);
+      own32[own_dst] = dec_pair(pair_lo);
+      own32[own_dst + 2] = dec_pair(pair_hi);
     }
     if (!last) {
       if (threadIdx.x < kCopyThreads && t > 0) copy_out(t - 1, hcp);
@@ -408,7 +421,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        if (eu + j < a.H) dst[j] = live ? hcur[j] : (_Float16)0.0f;
+        if (eu + 4 * j < a.H) dst[4 * j] = live ? hcur[j] : (_Float16)0.0f;
     }
     if (t + 1 == probe_next) {
       write_probe(probe_i);
@@ -453,7 +466,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     }
     asm volatile("" : "+v"(gn));
     gp = gn;
-    uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf);
+    uint32_t* hb32 = reinterpret_cast<uint32_t*>(hnext);
 #pragma unroll
     for (int r = 0; r < NW; ++r)
       if ((r >> 1) < nld) {
@@ -485,17 +498,17 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
         for (int j = 0; j < 8; ++j)
           if (k0 + j < a.H) v[j] = a.h0[((size_t)layer * a.B + gr) * a.H + k0 + j];
       }
-      hbuf[idx] = v;
+      hbuf[Tt & 1][idx] = v;
     }
     __syncthreads();
   }
-  // The last step's h (in hbuf after its gather) as the next layer's input.
-  if (ok && !last && Tt > 0 && threadIdx.x < kCopyThreads) copy_out(Tt - 1, hbuf[copy_src]);
+  // The last step's h (in hbuf[Tt & 1] after its gather) as the next layer's input.
+  if (ok && !last && Tt > 0 && threadIdx.x < kCopyThreads) copy_out(Tt - 1, hbuf[Tt & 1][copy_src]);
 
   if (!ok) {
     // A wait failed, here or in an earlier layer's launch (the status word records it): poison every
     // output of this workgroup (states, probes, output sequence, head) and leave.
-    if (row_ok) poison_lane_outputs(a, layer, grow, eu, 2, last);
+    if (row_ok) poison_lane_outputs(a, layer, grow, eu, 2, last, 4);
     if (last && slice == 0 && a.out) {
       for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
         const int gr = a.row0 + tile * 16 + idx / a.O;
@@ -511,7 +524,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        if (eu + j < a.H) dst[j] = (_Float16)0.0f;
+        if (eu + 4 * j < a.H) dst[4 * j] = (_Float16)0.0f;
     }
   }
   // ... and the next layer's input there is the frozen state (its rows are frozen as well).
@@ -522,7 +535,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   if (row_ok) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int u = eu + j;
+      const int u = eu + 4 * j;
       if (u < a.H) {
         const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
         if (a.h_n) a.h_n[si] = hcur[j];
@@ -530,13 +543,13 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       }
     }
   }
-  // Linear head (last layer, first slice) on the full final h held in hbuf.
+  // Linear head (last layer, first slice) on the full final h held in hbuf[Tt & 1].
   if (last && slice == 0 && a.out) {
     for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
       const int rr = idx / a.O, o = idx % a.O;
       const int gr = a.row0 + tile * 16 + rr;
       if (gr >= a.row_end) continue;
-      const _Float16* hf = reinterpret_cast<const _Float16*>(hbuf);
+      const _Float16* hf = reinterpret_cast<const _Float16*>(hbuf[Tt & 1]);
       const float* wr = a.wlin + (size_t)o * HP;
       float s0 = 0.f, s1 = 0.f;
       for (int k8 = 0; k8 < HP; k8 += 8) {
@@ -559,7 +572,7 @@ inline unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per 
 hipError_t launch_pack_rec_layer(const Geometry& g, int layer, const _Float16* w_hh, _Float16* wpack, hipStream_t s) {
   if (g.HP != 512) return hipErrorInvalidValue;
   using C = Rec<512>;
-  const size_t per_layer = (size_t)C::kS * 8 * C::kKcw * 4 * 64 * 8;
+  const size_t per_layer = (size_t)C::kS * 8 * C::kKch * 2 * 64 * 8;
   hipLaunchKernelGGL(pack_rec_kernel<512>, blocks_for(per_layer, 256), 256, 0, s, w_hh, g.H, wpack + layer * per_layer);
   return hipGetLastError();
 }

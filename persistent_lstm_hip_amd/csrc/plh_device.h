@@ -113,23 +113,19 @@ __device__ __forceinline__ float pick(bool sel, float a, float b) {
 }
 
 // Work split of the sliced kernels (H 129..512): S workgroups ("slices") per (layer, 16-row tile),
-// each holding the gate rows of HS hidden units.
+// each holding the gate rows of HS hidden units for both the layer input and h.  Wave w of a slice
+// owns 4 NJ units (HS = 32 NJ) over all of K: NJ MFMA A tiles of 16 gate rows each (row r of tile j
+// is gate r % 4 of unit 4 NJ w + 4 j + r / 4) for 2 KCH K-chunks, KCH of W_ih then KCH of W_hh,
+// i.e. 2 KCH NJ = 32 fragments (128 VGPRs) at both padded sizes.
 template <int HP>
 struct Sliced {
-  static constexpr int kKsp = HP / 256;     // waves per K part of a unit group
-  static constexpr int kGroups = 4 / kKsp;  // 16-unit groups per workgroup
-  static constexpr int kHs = 16 * kGroups;  // hidden units per workgroup
-  static constexpr int kS = HP / kHs;       // workgroups per (layer, tile)
-  static constexpr int kKch = HP / 32;      // K chunks of one part
-  static constexpr int kWpg = 2 * kKsp;     // waves per unit group
-  static constexpr int kWords = HP * 8;     // tagged words of one step's h of a 16-row tile
-  // Wave roles: waves 0..3 hold W_ih parts, waves 4..7 W_hh parts, so each SIMD (wave w % 4) runs one
-  // of each and the input waves' MFMAs for step t+1 overlap the recurrent critical path of step t.
-  // Wave w serves unit group (w % 4) / KSP as member e = (w / 4) * KSP + w % KSP of the group
-  // (e < KSP: input part, quarter e; else recurrent part, quarter e - KSP).
-  static __host__ __device__ constexpr int group_of(int w) { return (w & 3) / kKsp; }
-  static __host__ __device__ constexpr int member_of(int w) { return (w >> 2) * kKsp + (w & (kKsp - 1)); }
-  static __host__ __device__ constexpr int wave_of(int g, int e) { return (e / kKsp) * 4 + g * kKsp + e % kKsp; }
+  static constexpr int kS = HP == 256 ? 4 : 16;  // workgroups per (layer, tile)
+  static constexpr int kHs = HP / kS;            // hidden units per workgroup: 64 or 32
+  static constexpr int kNj = kHs / 32;           // A tiles per wave: 2 or 1
+  static constexpr int kKch = HP / 32;           // K chunks of the layer input and of h
+  static constexpr int kWords = HP * 8;          // ring words reserved per step slot of a tile (the
+                                                 // packed words of one step take half)
+  static_assert(HP == 256 || HP == 512, "padded H 256 or 512");
 };
 
 // Work split of the layer-sequential recurrent kernel (padded H = 512, plh_rec.hip): the input
@@ -149,14 +145,36 @@ struct Rec {
 // ---- tagged exchange of h among the workgroups of a tile (plh_sliced.hip; plh_rec.hip shares
 // sliced_coords and packs its words itself) ----
 
-__device__ __forceinline__ uint64_t tag_word(_Float16 a, _Float16 b, uint32_t tag) {
-  union { _Float16 h[2]; uint32_t u; } v;
-  v.h[0] = a;
-  v.h[1] = b;
-  return (uint64_t)v.u | ((uint64_t)tag << 32);
+// Packed exchange words.  A 64-bit word carries 4 fp16 h of one batch row and a 4-bit step tag, one
+// tag bit in bit 14 (the exponent's top bit) of each fp16.  That bit is clear in every h a step
+// computes (|h| <= 1 < 2); NaN and infinity, the only other values with it set, travel as +-1.5
+// (never an h) and come back as NaN.  The bit is cleared in every value sent, so the tag is always
+// intact.  Rows of length 0 keep their h0, which may use the bit: their exchanged values only feed
+// their own frozen rows, and the kernels restore h0 before it is read as a result.
+__device__ __forceinline__ uint32_t xw_enc_half(uint32_t b) {
+  return (b & 0x7C00u) == 0x7C00u ? (b & 0x8000u) | 0x3E00u : b & 0xBFFFu;
 }
-
-__device__ __forceinline__ uint32_t word_tag(uint64_t w) { return (uint32_t)(w >> 32); }
+__device__ __forceinline__ uint32_t xw_enc_half(_Float16 h) { return xw_enc_half((uint32_t)__builtin_bit_cast(uint16_t, h)); }
+__device__ __forceinline__ uint32_t xw_enc_pair(uint32_t p) {
+  return xw_enc_half(p & 0xFFFFu) | (xw_enc_half(p >> 16) << 16);
+}
+// Two fp16 of a word back, the tag bits cleared and +-1.5 restored as NaN.
+__device__ __forceinline__ uint32_t xw_dec_pair(uint32_t v) {
+  uint32_t x = v & 0xBFFFBFFFu;
+  if ((x & 0x7FFFu) == 0x3E00u) x |= 0x7E00u;
+  if ((x & 0x7FFF0000u) == 0x3E000000u) x |= 0x7E000000u;
+  return x;
+}
+__device__ __forceinline__ uint32_t xw_tag(uint64_t w) {
+  return (uint32_t)(((w >> 14) & 1u) | ((w >> 29) & 2u) | ((w >> 44) & 4u) | ((w >> 59) & 8u));
+}
+__device__ __forceinline__ uint64_t xw_tag_bits(uint32_t tag) {
+  return ((uint64_t)(tag & 1u) << 14) | ((uint64_t)((tag >> 1) & 1u) << 30) | ((uint64_t)((tag >> 2) & 1u) << 46) |
+         ((uint64_t)((tag >> 3) & 1u) << 62);
+}
+// Tag of step t's words in a two-slot ring (slot t & 1): successive writes to a slot (steps t - 2
+// and t) differ, and none is 0 (the cleared ring).
+__device__ __forceinline__ uint32_t xw_step_tag(int t) { return (uint32_t)((t >> 1) % 15) + 1u; }
 
 __device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -34,6 +34,12 @@ struct Geometry {
   int kp0, kp;  // K of the projection GEMM, padded to a multiple of 128: layer 0 (0 with rec_x0), layers >= 1
 };
 
+// u32 words per (layer, tile) counter: the sliced kernels' counters each take a 128-byte line of
+// their own (their workgroups read and update them every few steps, and counters sharing a line
+// serialise those accesses); the wavefront kernels' are adjacent.
+constexpr int kSlicedCounterStride = 32;
+inline int counter_stride(const Geometry& g) { return g.slices > 1 && !g.rec ? kSlicedCounterStride : 1; }
+
 // Fills *g; returns false (with the reason) for geometries the kernels do not implement.
 bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why);
 // g (rec_ok) switched to the layer-sequential path.
@@ -42,7 +48,7 @@ Geometry as_layer_sequential(const Geometry& g);
 // Byte offsets of the packed-weight blob (all 256-byte aligned).
 struct PackedLayout {
   size_t wpack;  // f16 MFMA A fragments of every lane: [L][waves][kc][4 gates][64 lanes][8], or when
-                 // sliced [L][slices][8 waves][8 chunks][4 gates][64 lanes][8]
+                 // sliced [L][slices][8 waves][2 KCH chunks][NJ tiles][64 lanes][8] (Sliced<HP>)
   size_t bias;   // f32 [L][4][HP]: b_ih + b_hh
   size_t wlin;   // f32 [O][HP]
   size_t blin;   // f32 [O]
@@ -59,7 +65,7 @@ PackedLayout packed_layout(const Geometry& g);
 
 // Workspace of one persistent launch (reused by successive batch chunks); R = rows per tile:
 //   status   u32                                   PLH_STATUS_* bits
-//   counters u32 [L][ntile]                        steps published per (layer, tile)
+//   counters u32 [L][ntile][counter_stride]       progress published per (layer, tile)
 //   xp       f16x8 [ntile][T][g_in0][R]            x in B-fragment order (layer 0 input): group g
 //                                                  holds k = 8g .. 8g+7, the first g_in0 * R
 //                                                  entries of a step's fragment blocks
@@ -95,7 +101,7 @@ struct ForwardArgs {
   f16x8_t* xp;                  // packed x, see WorkspaceLayout
   f16x8_t* hseq;                // inter-layer hand-off, see WorkspaceLayout
   uint64_t* xring;              // sliced kernels: tagged h exchange ring, zeroed before each launch
-  uint32_t* counters;           // [L][ntile] steps published per (layer, tile)
+  uint32_t* counters;           // [L][ntile][counter_stride] progress published per (layer, tile)
   uint32_t* status;             // PLH_STATUS_* bits
   const _Float16* h0;           // [L, B, H] or null
   const _Float16* c0;

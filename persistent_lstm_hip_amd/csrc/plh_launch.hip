@@ -89,7 +89,7 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   w.tile_rows = tile_rows;
   w.status = 0;
   w.counters = 256;
-  w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile);
+  w.xp = align256(w.counters + sizeof(uint32_t) * (size_t)g.L * ntile * counter_stride(g));
   if (g.rec) {
     // xp (rec_x0 only) holds x as [ntile][T][4][16] f16x8
     w.hseq = w.xring = align256(w.xp + (g.rec_x0 ? ntile * seq_len * 4 * 16 * 16 : 0));

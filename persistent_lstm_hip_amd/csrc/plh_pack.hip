@@ -40,31 +40,34 @@ __global__ void pack_layer_kernel(const _Float16* __restrict__ w_ih, const _Floa
   dst[e] = v;
 }
 
-// Sliced weights: [L][S][8 waves][8 chunks][4 gates][64 lanes][8].  Wave w of slice s holds unit
-// group Sliced::group_of(w); member e = Sliced::member_of(w) selects the part e / KSP (0: W_ih,
-// 1: W_hh) and the quarter e % KSP of that part's columns.
+// Sliced weights: [L][S][8 waves][2 KCH chunks][NJ tiles][64 lanes][8].  Wave w of slice s holds
+// the gate rows of its 4 NJ units s HS + 4 NJ w + 0 .. 4 NJ - 1 over all of K: chunks 0 .. KCH - 1
+// of W_ih (the layer input, zero past K), then KCH chunks of W_hh; row r of tile j is gate r % 4 of
+// unit s HS + 4 NJ w + 4 j + r / 4, and lane l of chunk kc holds k = 32 kc + 8 (l / 16) + 0 .. 7.
 template <int HP>
 __global__ void pack_sliced_kernel(const _Float16* __restrict__ w_ih, const _Float16* __restrict__ w_hh, int K,
                                    int H, _Float16* __restrict__ dst) {
   using C = Sliced<HP>;
-  const size_t total = (size_t)C::kS * 8 * 8 * 4 * 64 * 8;
+  constexpr int NJ = C::kNj, KCH = C::kKch;
+  const size_t total = (size_t)C::kS * 8 * 2 * KCH * NJ * 64 * 8;
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= total) return;
-  const int j = e & 7;
+  const int jj = e & 7;
   const int lane = (e >> 3) & 63;
-  const int q = (e >> 9) & 3;
-  const int kc = (int)((e >> 11) & 7);
-  const int wv = (int)((e >> 14) & 7);
-  const int sl = (int)(e >> 17);
-  const int g = C::group_of(wv), ew = C::member_of(wv);
-  const bool rec = ew >= C::kKsp;
-  const int kq = ew % C::kKsp;
-  const int u = sl * C::kHs + g * 16 + (lane & 15);
-  const size_t col = (size_t)q * H + u;
-  const int k = (kq * 8 + kc) * 32 + (lane >> 4) * 8 + j;
+  size_t rest = e >> 9;
+  const int j = (int)(rest % NJ);
+  rest /= NJ;
+  const int kc = (int)(rest % (2 * KCH));
+  rest /= 2 * KCH;
+  const int wv = (int)(rest % 8);
+  const int sl = (int)(rest / 8);
+  const int r = lane & 15;
+  const int u = sl * C::kHs + wv * 4 * NJ + 4 * j + (r >> 2);
+  const size_t col = (size_t)(r & 3) * H + u;
+  const int k = (kc % KCH) * 32 + (lane >> 4) * 8 + jj;
   _Float16 v = (_Float16)0.0f;
   if (u < H) {
-    if (!rec) {
+    if (kc < KCH) {
       if (k < K) v = w_ih[col * K + k];
     } else {
       if (k < H) v = w_hh[col * H + k];
@@ -175,7 +178,7 @@ hipError_t launch_forward_prologue(const Geometry& g, const ForwardArgs& a, uint
                                    size_t ring_words, hipStream_t s) {
   const size_t npack = (size_t)a.ntile * a.T * g0 * a.tile_rows;
   const size_t nstat = status ? 1 : 0;
-  const size_t nctr = (size_t)g.L * a.ntile;
+  const size_t nctr = (size_t)g.L * a.ntile * counter_stride(g);
   const size_t nring = ring_words * 2;  // u64 words as u32
   const size_t n = std::max(std::max(npack, nstat), std::max(nctr, nring));
   if (n == 0) return hipSuccess;

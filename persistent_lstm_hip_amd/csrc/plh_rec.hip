@@ -231,14 +231,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     return gsrc[tc * a.ntile * (4 * HP / 32) * 64];
   };
 
-  // Packed exchange.  A word carries 4 fp16 of one row: units eu, eu + 1 (low half) and eu + 4,
-  // eu + 5 (high half) of a lane with even kgx, which holds eu and eu + 4 and takes eu + 1 and eu + 5
-  // from its partner lane + 16, and a 4-bit step tag in bit 14 of each fp16.  That bit is clear in every h a step computes (|h| <= 1 < 2); NaN and
-  // infinity, the only other values with it set, travel as +-1.5 (never an h) and come back as NaN.
-  // The bit is cleared in every value sent, so the tag is always intact; rows of length 0 keep their
-  // h0, which may use it: their exchanged values only feed their own (frozen) rows and are restored
-  // from h0 before they are read as results.  Half the bytes of one word per pair with a 32-bit
-  // tag.  Words are in writer order [slice][wave][32].
+  // Packed exchange (xw_* words): a word carries units eu, eu + 1 (low half) and eu + 4, eu + 5 (high
+  // half) of one row from a lane with even kgx, which holds eu and eu + 4 and takes eu + 1 and eu + 5
+  // from its partner lane + 16.  Half the bytes of one word per pair with a 32-bit tag.  Words are in
+  // writer order [slice][wave][32].
   uint64_t* ring = a.xring + (size_t)tile * 2 * C::kWords;  // a slot of PW words per step parity
   const int pwoff = (slice * 8 + wave) * 32 + (kgx >> 1) * 16 + en;  // this lane's word (even kgx)
   // A workgroup gathers the 7 sibling slices' words (its own pairs go to hbuf from registers): load
@@ -259,20 +255,6 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     return ((eu_ >> 3) * 16 + en_) * 4 + ((eu_ & 7) >> 1);
   };
   const int own_dst = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's word's first pair in hbuf (even kgx)
-  auto enc_half = [](_Float16 h) -> uint32_t {
-    const uint32_t b = __builtin_bit_cast(uint16_t, h);
-    return (b & 0x7C00u) == 0x7C00u ? (b & 0x8000u) | 0x3E00u : b & 0xBFFFu;
-  };
-  auto dec_pair = [](uint32_t v) -> uint32_t {
-    uint32_t x = v & 0xBFFFBFFFu;
-    if ((x & 0x7FFFu) == 0x3E00u) x |= 0x7E00u;
-    if ((x & 0x7FFF0000u) == 0x3E000000u) x |= 0x7E000000u;
-    return x;
-  };
-  auto ptag = [](uint64_t w) -> uint32_t {
-    return (uint32_t)(((w >> 14) & 1u) | ((w >> 29) & 2u) | ((w >> 44) & 4u) | ((w >> 59) & 8u));
-  };
-
   // b_ih + b_hh of this lane's units (eu + 4 j) by gate, in registers for the whole sequence.
   float bias[4][2];
 #pragma unroll
@@ -368,7 +350,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // output sequence, probes, the next step's input projection): loads and stores retire in issue
     // order, so the poll waits for nothing issued after it.
     // Tags of successive writes to a slot (steps t - 2, t) differ, and none is 0 (the cleared ring).
-    const uint32_t want = (uint32_t)((t >> 1) % 15) + 1u;
+    const uint32_t want = xw_step_tag(t);
     // This step's ring slot, uniform by construction: the compiler would otherwise keep its address
     // in VGPRs (it flows through the lane-conditional store) and put every poll in a waterfall loop.
     uint64_t* const slot = ring + (size_t)__builtin_amdgcn_readfirstlane(t & 1) * PW;
@@ -376,13 +358,11 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // partner lane + 16 (kgx + 1) eu + 1 and eu + 5.
     uint32_t pair_lo, pair_hi;
     {
-      const uint32_t mine = enc_half(hcur[0]) | (enc_half(hcur[1]) << 16);
+      const uint32_t mine = xw_enc_half(hcur[0]) | (xw_enc_half(hcur[1]) << 16);
       const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
       pair_lo = __builtin_amdgcn_perm(other, mine, 0x05040100u);
       pair_hi = __builtin_amdgcn_perm(other, mine, 0x07060302u);
-      const uint64_t tagbits = ((uint64_t)(want & 1u) << 14) | ((uint64_t)((want >> 1) & 1u) << 30) |
-                               ((uint64_t)((want >> 2) & 1u) << 46) | ((uint64_t)((want >> 3) & 1u) << 62);
-      const uint64_t word = ((uint64_t)pair_lo | ((uint64_t)pair_hi << 32)) | tagbits;
+      const uint64_t word = ((uint64_t)pair_lo | ((uint64_t)pair_hi << 32)) | xw_tag_bits(want);
       if ((kgx & 1) == 0) {
         if (l2)
           __hip_atomic_store(slot + pwoff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -419,8 +399,8 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // in step t).
     if ((kgx & 1) == 0) {
       uint32_t* own32 = reinterpret_cast<uint32_t*>(hnext);
-      own32[own_dst] = dec_pair(pair_lo);
-      own32[own_dst + 2] = dec_pair(pair_hi);
+      own32[own_dst] = xw_dec_pair(pair_lo);
+      own32[own_dst + 2] = xw_dec_pair(pair_hi);
     }
     if (!last) {
       if (threadIdx.x < kCopyThreads && t > 0) copy_out(t - 1, hcp);
@@ -441,7 +421,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < NW; ++r) ready = ready && ((r >> 1) >= nld || ptag(wv[r]) == want);
+      for (int r = 0; r < NW; ++r) ready = ready && ((r >> 1) >= nld || xw_tag(wv[r]) == want);
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -459,7 +439,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
       for (int p = 0; p < NW / 2; ++p)
-        if (p < nld && (ptag(wv[2 * p]) != want || ptag(wv[2 * p + 1]) != want)) pload(p);
+        if (p < nld && (xw_tag(wv[2 * p]) != want || xw_tag(wv[2 * p + 1]) != want)) pload(p);
     }
     // gn's load was issued before this step's poll, so it has completed (loads retire in order);
     // the empty asm tells the compiler, which would otherwise count the copy below as a read of a
@@ -478,8 +458,8 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     for (int r = 0; r < NW; ++r)
       if ((r >> 1) < nld) {
         const int d = gdst(r);
-        hb32[d] = dec_pair((uint32_t)wv[r]);
-        hb32[d + 2] = dec_pair((uint32_t)(wv[r] >> 32));
+        hb32[d] = xw_dec_pair((uint32_t)wv[r]);
+        hb32[d + 2] = xw_dec_pair((uint32_t)(wv[r] >> 32));
       }
     lds_barrier();
     return __builtin_amdgcn_readfirstlane(s_fail) == 0;

@@ -3,64 +3,68 @@
 //
 // Hidden sizes above 128.  A layer's [W_ih | W_hh] (1 MB at H = 256, 4 MB at H = 512) no longer fits
 // one CU's register file, so each (layer, 16-row tile) is served by S workgroups ("slices"), each
-// keeping the gate rows of HS = HP / S hidden units resident in VGPRs:
-//   * the 8 waves of a slice form HS/16 unit groups; within a group, KSP waves hold the input part
-//     (W_ih columns, 256 per wave) and KSP waves the recurrent part (W_hh columns), so every wave's
-//     resident weights are 8 K-chunks x 4 gates = 128 VGPRs;
-//   * per step each wave computes its partial gate sums with MFMA, the partials meet in LDS, and
-//     the group's waves split the gate math of its 16 units x 16 rows (two units per lane);
-//   * the slices exchange h_t every step through a small ring of tagged words (below); the next
-//     layer still receives h through the hand-off buffer and a per-(layer, tile) step counter
-//     published once per chunk, so layers run as a wavefront.
+// keeping the gate rows of HS = HP / S hidden units resident in VGPRs (Sliced<HP>):
+//   * wave w of a slice owns 4 NJ units over all of K (the layer input and h): its A tiles
+//     interleave the gates (row r: gate r % 4 of unit 4 j + r / 4), so the D fragments give each
+//     lane all four gates of its units eu + 4 j for one row, and the cell update needs no other
+//     wave: no partial sums cross waves;
+//   * a step's gate sums are one MFMA chain per tile that starts from the bias: the input part
+//     x_t W_ih^T is computed a phase ahead (off the critical path, from the layer input staged in
+//     LDS), and only h_{t-1} W_hh^T (KCH NJ MFMAs per wave) sits between a step's exchange and its
+//     cell update;
+//   * the slices exchange h_t every step through a two-slot ring of tagged 64-bit words (the xw_*
+//     words of plh_device.h: 4 fp16 and a 4-bit step tag each); a reader polls every slice's
+//     words (its own included) until their tags are the step's, with no counter or barrier between
+//     a slice's cell update and its siblings' next step.  When the S slices of a group run on one
+//     XCD (checked at entry) the words are stored without sc1 and stay in its L2 (same_xcd_group);
+//   * with two tiles per workgroup (NTI = 2) the tiles alternate phases: a tile's exchange runs
+//     while the other tile computes, and one workgroup barrier per phase orders LDS;
+//   * layers run as a wavefront.  h_t also goes to the hand-off buffer (hseq, fragment order, sc1
+//     stores); each wave publishes its stores per group of G steps with one atomic add to the
+//     (layer, tile) counter, and the next layer's waves check that counter (prefetched a phase
+//     ahead) before they load an input step, D steps before it is used, in 1 KB pieces staged
+//     through registers into a two-slot LDS ring.
 //
-// Tagged exchange.  One step's h of a tile is HP x 16 halfs, stored as 64-bit words
-// {h[u], h[u+1], tag = t + 1} in writer order ([slice][wave][lane], one word per active lane), so
-// each wave's stores and each reader's loads cover contiguous 512-byte runs; the reader scatters
-// the payloads into B-fragment order in LDS.  A reader spins on
-// the words themselves until every tag it needs equals t + 1: no store-completion wait, barrier or
-// counter round trip sits between a slice's epilogue and its siblings' next step.  Every word is
-// written and read with agent-scope relaxed 64-bit atomics (sc1), which are single-copy atomic and
-// coherent across the XCDs' L2 caches without cache maintenance; when all slices of a group run on
-// one XCD (checked at entry) the words are stored without sc1 and stay in its L2 (same_xcd_group).  Two ring slots suffice: a slice
-// can overwrite slot t % 2 with h_{t+2} only after it has read h_{t+1} of every sibling, and a
-// sibling writes h_{t+1} only after it has read h_t from every slice.  The ring is zeroed before
-// each launch (tags start at 1).
+// Memory ordering rests on gfx950 retiring loads and stores on one counter in issue order: a wave
+// that has waited for its latest ring poll has also completed everything it issued before that
+// poll (its earlier hand-off stores, the input piece and the counter value it prefetched), so no
+// extra wait sits on the step.
 //
-// Hand-off to the next layer: h is also stored to the hand-off buffer with agent-scope relaxed
-// stores; at the end of each chunk every thread waits for its stores to complete (s_waitcnt)
-// before the barrier that precedes a relaxed counter increment.  The next layer reads the buffer
-// with ordinary loads after an agent-scope acquire, which invalidates any stale copy in its L2.
+// Reference behaviour restated (mantuoluozk/persistent_lstm_hip): the generic path's recurrence
+// (persistent_lstm_hip.cu:2923-3181) with the input projection kept in fp32, gate order i, f, g, o
+// and the c/h recurrence of persistent_lstm_reference.cpp:21-35.
 #include "plh_device.h"
 
 namespace plh {
 namespace {
 
-// NTI 16-row tiles per workgroup.  With NTI = 2 the two tiles are software-pipelined: a tile's
-// gather of h_t (issued right after its own words were stored) is completed in the middle of the
-// other tile's step, after that tile's gate math and before its stores, so the exchange latency
-// hides behind the other tile's work and the wait for the gather's loads (one in-order counter
-// covers loads and stores) finds only operations issued a whole phase earlier.
-// The layer hand-off is published every PUB chunks: the publication waits for every outstanding
-// memory operation of the workgroup (stores and gather loads share one counter), so publishing
-// less often keeps that wait off most steps.
-template <int HP, int CH, int NTI>
+template <int HP, int NTI>
 __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   using C = Sliced<HP>;
-  constexpr int KSP = C::kKsp, HS = C::kHs, S = C::kS, KCH = C::kKch, WPG = C::kWpg;
-  constexpr int NT = 512, FV = 64;                  // 16-row fragment blocks
-  constexpr int RN = (CH * KCH * FV + NT - 1) / NT;  // f16x8 of a chunk's input each thread moves
-  constexpr int KCW = 8;                            // K chunks per wave
-  constexpr int PUB = NTI == 1 ? 1 : 4;             // chunks per hand-off publication
-  static_assert(KCH * FV % NT == 0, "whole fragments per thread");
+  constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch, NJ = C::kNj;
+  constexpr int NT = 512, FV = 64;        // 16-row fragment blocks: 64 lanes x 16 bytes
+  constexpr int UPW = 4 * NJ;             // hidden units per wave
+  constexpr int KW = 4 / NJ;              // lanes with kgx % KW == 0 send a word
+  constexpr int SB = 4 * HS;              // packed words of one slice per step
+  constexpr int PW = S * SB;              // packed words of one step of a tile (4 HP)
+  constexpr int NLD = PW / 2 / NT;        // 16-byte poll loads per thread and step
+  constexpr int D2 = NJ == 2 ? 2 : 1;     // u32 distance in hbuf between a word's two pairs
+  constexpr int BPW = KCH / 8;            // 1 KB input blocks each wave stages per step
+  constexpr int G = 2;                    // steps per publication of the hand-off
+  constexpr int D = 3;                    // steps between an input's load and its use
+  constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every range: stores dropped
+  // Memory operations issued after a poll before its gather: with two tiles the input pieces and
+  // the counter load, with one the hand-off stores.
+  constexpr int kAfterPoll = NTI == 2 ? BPW + 1 : (NJ == 2 ? 2 : 1);
+  static_assert(kAfterPoll < 16, "vmcnt field");
   static_assert(NTI == 1 || NTI == 2, "one or two tiles per workgroup");
+  static_assert(PW % (2 * NT) == 0 && KCH % 8 == 0, "whole loads per thread");
 
-  __shared__ f16x8 ring[NTI][CH * KCH * FV];  // step inputs of the current chunk (all HP input units)
-  __shared__ f16x8 hbuf[NTI][KCH * FV];       // h_{t-1} of all HP units
-  // Partial gate sums of every wave: per tile with two tiles (the other tile's gather barrier
-  // separates a tile's epilogue from the next writes), double-buffered by step with one.
-  __shared__ f32x4 part[2][8][4][64];
-  __shared__ float2 s_bias[4][HS / 2];  // b_ih + b_hh of this slice's units, by gate and unit pair
-  __shared__ int s_ok[2];
+  // h_{t-1} in fragment order: per tile with two tiles (a tile's h is gathered while the other
+  // tile computes), double-buffered by step parity with one.
+  __shared__ f16x8 hbuf[2][KCH * FV];
+  __shared__ f16x8 ring[NTI][2][KCH * FV];  // layer input x_t of tile i in slot t & 1
+  __shared__ float s_bias[4][HS];
   __shared__ int s_fail;
   __shared__ int s_tlen;
   __shared__ int s_l2;
@@ -69,18 +73,13 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   const int lane = threadIdx.x & 63;
   int layer, tgrp, slice;
   sliced_coords(blockIdx.x, a.ntile / NTI, S, a.xcd_map, layer, tgrp, slice);
-  const int g = C::group_of(wave), ew = C::member_of(wave);
-  const bool recurrent = ew >= KSP;  // this wave holds W_hh columns
-  const int kq = ew % KSP;           // which 256-column quarter of its part
-
-  // Epilogue mapping: each active lane evaluates units eu, eu + 1 of row en.  The partial sums of
-  // (unit 4 kgx + i, row en) sit in element i of lane 16 kgx + en of every wave of the group.
-  const int en = lane & 15;
-  const int kgx = WPG == 2 ? (lane >> 4) : ew;
-  const int pp = WPG == 2 ? ew : ((lane >> 4) & 1);
-  const bool active = WPG == 2 || lane < 32;
-  const int pl = kgx * 16 + en;
-  const int eu = slice * HS + g * 16 + kgx * 4 + 2 * pp;
+  const int en = lane & 15, kgx = lane >> 4;
+  // This lane's units eu + 4 j (j < NJ) of row en: all four gates of each are in its D fragments.
+  const int eu = slice * HS + wave * UPW + kgx;
+  const bool writer = kgx % KW == 0;
+  const int tile0 = tgrp * NTI;  // first 16-row tile of this workgroup
+  const bool has_up = layer > 0;
+  const bool has_down = layer + 1 < a.L;
 
   int grow[NTI], len[NTI];
   bool row_ok[NTI];
@@ -103,7 +102,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   const bool l2 = __builtin_amdgcn_readfirstlane(s_l2) != 0;
 #pragma unroll
   for (int i = 0; i < NTI; ++i) {
-    grow[i] = a.row0 + (tgrp * NTI + i) * 16 + en;
+    grow[i] = a.row0 + (tile0 + i) * 16 + en;
     row_ok[i] = grow[i] < a.row_end;
     len[i] = 0;
     if (row_ok[i]) {
@@ -113,196 +112,289 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     if (wave == 0 && lane < 16) atomicMax(&s_tlen, len[i]);
   }
   __syncthreads();
-  const int Tt = s_tlen;  // steps of this workgroup: the longest row of its tiles
+  // Steps of this workgroup: the longest row of its tiles (the same in every layer).
+  const int Tt = __builtin_amdgcn_readfirstlane(s_tlen);
 
-  f16x8 w[KCW][4];
+  // Resident weights: chunks 0 .. KCH - 1 of W_ih, then KCH of W_hh, NJ tiles each.
+  f16x8 w[2 * KCH][NJ];
   {
     const f16x8* wp = reinterpret_cast<const f16x8*>(a.wpack) +
-                      ((size_t)((layer * S + slice) * 8 + wave) * KCW * 4) * 64 + lane;
+                      (size_t)((layer * S + slice) * 8 + wave) * 2 * KCH * NJ * 64 + lane;
 #pragma unroll
-    for (int kc = 0; kc < KCW; ++kc)
+    for (int kc = 0; kc < 2 * KCH; ++kc)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) w[kc][q] = wp[(kc * 4 + q) * 64];
+      for (int j = 0; j < NJ; ++j) w[kc][j] = wp[(kc * NJ + j) * 64];
   }
-  // Wait for the resident weights here: otherwise the compiler keeps them "possibly outstanding"
-  // into the step loop and puts vmcnt waits before the input waves' MFMAs, which (one in-order
-  // counter on gfx950) then wait for the gather loads those MFMAs are meant to overlap.
+  // The resident weights complete here (otherwise the compiler keeps them "possibly outstanding"
+  // and waits for every global access in flight before the step loop's MFMAs).
   __builtin_amdgcn_s_waitcnt(0);
-  for (int idx = threadIdx.x; idx < 4 * HS / 2; idx += NT) {
-    const int q = idx / (HS / 2), up = idx % (HS / 2);
-    const float* b = a.bias + ((size_t)layer * 4 + q) * HP + slice * HS + 2 * up;
-    s_bias[q][up] = float2{b[0], b[1]};
+  for (int idx = threadIdx.x; idx < 4 * HS; idx += NT) {
+    const int q = idx / HS, u = idx % HS;
+    s_bias[q][u] = a.bias[((size_t)layer * 4 + q) * HP + slice * HS + u];
   }
 
-  float c[NTI][2];
-  _Float16 hcur[NTI][2];
+  float c[NTI][NJ];
+  _Float16 hcur[NTI][NJ];
 #pragma unroll
   for (int i = 0; i < NTI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int u = eu + j;
+    for (int j = 0; j < NJ; ++j) {
+      const int u = eu + 4 * j;
       const bool v = row_ok[i] && u < a.H;
       const size_t si = ((size_t)layer * a.B + grow[i]) * a.H + u;
       c[i][j] = (v && a.c0) ? (float)a.c0[si] : 0.0f;
       hcur[i][j] = (v && a.h0) ? a.h0[si] : (_Float16)0.0f;
     }
-  // h_{-1} of all units into hbuf (fragment order)
-  for (int idx = threadIdx.x; idx < NTI * KCH * FV; idx += NT) {
-    const int i = idx / (KCH * FV), kc = idx / FV % KCH, l = idx % FV;
-    const int gr = a.row0 + (tgrp * NTI + i) * 16 + (l & 15);
-    const int k0 = kc * 32 + (l >> 4) * 8;
-    f16x8 v = {};
-    if (a.h0 && gr < a.row_end) {
+  // h_{-1} of all units into hbuf (fragment order), and a zero input ring.
+  auto fill_h0 = [&](int i, f16x8* dst) {
+    for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) {
+      const int kc = idx / FV, l = idx % FV;
+      const int gr = a.row0 + (tile0 + i) * 16 + (l & 15);
+      const int k0 = kc * 32 + (l >> 4) * 8;
+      f16x8 v = {};
+      if (a.h0 && gr < a.row_end) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (k0 + j < a.H) v[j] = a.h0[((size_t)layer * a.B + gr) * a.H + k0 + j];
+        for (int j = 0; j < 8; ++j)
+          if (k0 + j < a.H) v[j] = a.h0[((size_t)layer * a.B + gr) * a.H + k0 + j];
+      }
+      dst[idx] = v;
     }
-    hbuf[i][idx % (KCH * FV)] = v;
-  }
+  };
+#pragma unroll
+  for (int i = 0; i < NTI; ++i) fill_h0(i, hbuf[i]);
+  for (int idx = threadIdx.x; idx < NTI * 2 * KCH * FV; idx += NT)
+    ring[idx / (2 * KCH * FV)][(idx / (KCH * FV)) & 1][idx % (KCH * FV)] = f16x8{};
+  __syncthreads();  // s_bias, hbuf and the ring complete
 
-  const bool has_up = layer > 0;
-  const bool has_down = layer + 1 < a.L;
-  const int per = has_up ? KCH * FV : a.g_in0 * 16;  // input f16x8 per step in the source
+  // b_ih + b_hh of this lane's units by gate, in registers for the whole sequence.
+  float bias[4][NJ];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) bias[q][j] = s_bias[q][wave * UPW + kgx + 4 * j];
+
+  // ---- layer input: staged into the LDS ring in 1 KB pieces, D steps ahead ----
+  // Every phase issues the same memory operations after its ring poll on every path (the
+  // hand-off stores, BPW piece loads and one counter load; lanes and layers without a use for one
+  // address it out of range or at a dummy word), so the next poll's wait counts them exactly and
+  // waits for the poll alone, not for the slower loads issued after it.
+  const int per = has_up ? KCH * FV : a.g_in0 * 16;  // f16x8 per step in the source
   const size_t hstep = (size_t)KCH * FV;
-  const int tile0 = tgrp * NTI;  // first 16-row tile of this workgroup
-  auto in_seq = [&](int i) -> const f16x8* {
-    return has_up ? a.hseq + ((size_t)(layer - 1) * a.ntile + tile0 + i) * a.T * hstep
-                  : a.xp + (size_t)(tile0 + i) * a.T * per;
+  // Descriptor of tile i's input of step s (word 3 0x00020000: DATA_FORMAT = 32 bit, which untyped
+  // buffer accesses need on CDNA).
+  auto in_rs = [&](int i, int s) {
+    const f16x8* src = has_up ? a.hseq + (((size_t)(layer - 1) * a.ntile + tile0 + i) * a.T + s) * hstep
+                              : a.xp + ((size_t)(tile0 + i) * a.T + s) * per;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<f16x8*>(src), 0, per * 16, 0x00020000);
   };
-  auto my_seq = [&](int i) -> f16x8* { return a.hseq + ((size_t)layer * a.ntile + tile0 + i) * a.T * hstep; };
-  auto xr = [&](int i) -> uint64_t* { return a.xring + ((size_t)layer * a.ntile + tile0 + i) * 2 * C::kWords; };
-  const int hoff = ((eu >> 3) * 16 + en) * 8 + (eu & 7);  // halfs: (row en, unit eu) in a step block
-  constexpr int WL = WPG == 2 ? 64 : 32;  // tagged words each wave writes per step (its active lanes)
-  constexpr int NW = C::kWords / NT;       // tagged words each thread gathers per step
-  static_assert(S * 8 * WL == C::kWords && C::kWords % NT == 0, "writer-order ring covers one step");
-  const int woff = (slice * 8 + wave) * WL + (lane & (WL - 1));  // this lane's word in a ring slot
-  // LDS destination (u32 index into hbuf) of the r-th word this thread gathers.
-  auto gdst = [&](int r) -> int {
-    const int wd = threadIdx.x + r * NT;
-    const int sl = wd / (8 * WL), wv_ = (wd / WL) % 8, ln = wd % WL;
-    const int g_ = C::group_of(wv_), ew_ = C::member_of(wv_);
-    const int kgx_ = WPG == 2 ? (ln >> 4) : ew_;
-    const int pp_ = WPG == 2 ? ew_ : ((ln >> 4) & 1);
-    const int eu_ = sl * HS + g_ * 16 + kgx_ * 4 + 2 * pp_;
-    return ((eu_ >> 3) * 16 + (ln & 15)) * 4 + ((eu_ & 7) >> 1);
-  };
-  auto up_ctr = [&](int i) -> const uint32_t* { return a.counters + (layer - 1) * a.ntile + tile0 + i; };
-  auto my_ctr = [&](int i) -> uint32_t* { return a.counters + layer * a.ntile + tile0 + i; };
-  const int sync_tid = 64;
-
-  const int nchunk = (Tt + CH - 1) / CH;
-  f16x8 R[NTI][RN];
-  // A step's source holds the first `per` of its KCH * FV ring entries (layer 0: the g_in0 8-wide K
-  // groups of x; the rest of the ring stays zero from the initialisation).
-  auto load_chunk = [&](int k) {
-    const int s0 = k * CH;
-    const int nel = min(CH, Tt - s0) * per;
+  // Input piece of tile i, step s: block wave * BPW + b of the step, one f16x8 per lane.  Entries
+  // past `per` (layer 0: x's K groups) read out of the descriptor's range, which returns zero.  The
+  // previous layer's h is read with sc1: it was written with sc1 by other CUs, and its counter was
+  // seen before the load is issued.
+  f16x8 pc[NTI][BPW];
+  auto load_piece = [&](int i, int s) {
+    const __amdgpu_buffer_rsrc_t rs = in_rs(i, s);
 #pragma unroll
-    for (int i = 0; i < NTI; ++i) {
-      const f16x8* src = in_seq(i) + (size_t)s0 * per;
-#pragma unroll
-      for (int r = 0; r < RN; ++r) {
-        const int idx = threadIdx.x + r * NT;
-        if (idx < nel) R[i][r] = src[idx];
-      }
+    for (int b = 0; b < BPW; ++b) {
+      const uint32_t off = (uint32_t)((wave * BPW + b) * FV + lane) * 16u;
+      if (has_up)
+        pc[i][b] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16));
+      else
+        pc[i][b] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     }
   };
-  auto store_chunk = [&](int k) {
-    const int nel = min(CH, Tt - k * CH) * per;
+  auto store_piece = [&](int i, int s) {
 #pragma unroll
-    for (int i = 0; i < NTI; ++i)
-#pragma unroll
-      for (int r = 0; r < RN; ++r) {
-        const int idx = threadIdx.x + r * NT;
-        if (idx < nel) ring[i][(idx / per) * (KCH * FV) + idx % per] = R[i][r];
-      }
-  };
-  // Slice-steps of the upstream tile published once its chunk k is complete (publications cover
-  // PUB chunks, or the whole sequence at its end).
-  auto need_up = [&](int k) -> uint32_t {
-    const int steps = ((k + PUB) / PUB) * PUB * CH;
-    return (uint32_t)(S * min(steps, Tt));
+    for (int b = 0; b < BPW; ++b) ring[i][s & 1][(wave * BPW + b) * FV + lane] = pc[i][b];
   };
 
-  int wait_idx = 0;
-  // Acquire chunk k of every tile of the upstream layer.  `poll` holds the last counter value the
-  // polling lane saw, per tile, so a chunk that was already published costs only the acquire fence.
-  uint32_t poll[NTI];
+  // ---- hand-off publication and its check by the next layer ----
+  // A (layer, tile) counter counts groups of G steps times the S slices: thread 0 of each slice
+  // adds a group once every wave of its workgroup has completed that group's hand-off stores.
+  // Wave 0 reads the upstream counter every phase of a tile (issued after the poll, used a phase
+  // of that tile later) and shares it in LDS; the other waves load a ring word nobody writes in
+  // its place.
+  constexpr int CS = kSlicedCounterStride;
+  auto up_ctr = [&](int i) -> uint32_t* { return a.counters + ((size_t)(layer - 1) * a.ntile + tile0 + i) * CS; };
+  auto my_ctr = [&](int i) -> uint32_t* { return a.counters + ((size_t)layer * a.ntile + tile0 + i) * CS; };
+  __shared__ uint32_t s_up[NTI];  // upstream counter of tile i as last read by wave 0
+  int pub[NTI];                   // groups of tile i published (thread 0)
+  int avail[NTI];                 // groups of tile i known published upstream (this wave)
+  uint32_t cup[NTI];              // wave 0: upstream counter of tile i, loaded a phase of the tile earlier
 #pragma unroll
-  for (int i = 0; i < NTI; ++i) poll[i] = 0;
-  auto acquire_up = [&](int k) -> bool {
-    const int slot = wait_idx++ & 1;
-    if (threadIdx.x == sync_tid) {
-      const uint32_t need = need_up(k);
-      int okv = 1;
-#pragma unroll
-      for (int i = 0; i < NTI; ++i) {
-        if (!okv) break;
-        if (poll[i] >= need) {
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-          okv = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u ? 1 : 0;
-        } else {
-          okv = wait_counter(up_ctr(i), need, a.status, a.wait_ticks);
+  for (int i = 0; i < NTI; ++i) {
+    pub[i] = 0;
+    avail[i] = 0;
+    cup[i] = 0;
+    if (threadIdx.x == 0) s_up[i] = 0;
+  }
+  auto load_counter = [&](int i) {
+    const uint32_t* p = (has_up && wave == 0)
+                            ? up_ctr(i)
+                            : reinterpret_cast<const uint32_t*>(a.xring + ((size_t)layer * a.ntile + tile0 + i) * 2 * C::kWords +
+                                                                C::kWords + PW + wave * 16);
+    cup[i] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  // Thread 0, after a phase's barrier: every wave has completed its hand-off stores of tile i's
+  // steps < t (issued before the poll it waited for in that phase).
+  auto publish = [&](int i, int t) {
+    const int groups = t >= Tt ? (Tt + G - 1) / G : t / G;
+    if (groups > pub[i]) {
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(my_ctr(i), (uint32_t)(groups - pub[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pub[i] = groups;
+    }
+  };
+  // Make step s of tile i's input available: its group published upstream.  The shared counter
+  // usually shows it; otherwise spin (bounded).  False if the wait failed.
+  auto need_input = [&](int i, int s) -> bool {
+    const int g = s / G;
+    if (g < avail[i]) return true;
+    const uint32_t need = (uint32_t)S * (uint32_t)(g + 1);
+    uint32_t v = __builtin_amdgcn_readfirstlane(*(volatile uint32_t*)&s_up[i]);
+    if (v < need) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      for (;;) {
+        v = __builtin_amdgcn_readfirstlane(__hip_atomic_load(up_ctr(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (v >= need) break;
+        if (__hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return false;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
+          __hip_atomic_fetch_or(a.status, PLH_STATUS_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          return false;
         }
-        poll[i] = __hip_atomic_load(up_ctr(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_sleep(8);
       }
-      s_ok[slot] = okv;
     }
-    __syncthreads();
-    return s_ok[slot] != 0;
+    avail[i] = (int)(v / (uint32_t)S);
+    return true;
   };
+  auto clamp_step = [&](int s) { return s < Tt ? s : Tt - 1; };
 
-  auto pslot = [&](int i, int t) -> int { return NTI == 2 ? i : (t & 1); };
-  // This wave's partial gate sums of tile i for step t: its K part of [ring slot s | h_{t-1}].
-  auto partials = [&](int i, int t, int s) {
-    const f16x8* src = (recurrent ? hbuf[i] : ring[i] + s * (KCH * FV)) + kq * KCW * FV + lane;
-    f32x4 acc[4];
+  // ---- MFMA parts of a step ----
+  f32x4 acc[NTI][NJ];
+  // acc[i] = bias + x_s W_ih^T of tile i (x_s in ring slot s & 1).
+  auto input_mfma = [&](int i, int s) {
+    const f16x8* src = ring[i][s & 1] + lane;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{bias[0][j], bias[1][j], bias[2][j], bias[3][j]};
 #pragma unroll
-    for (int kc = 0; kc < KCW; ++kc) {
+    for (int kc = 0; kc < KCH; ++kc) {
       const f16x8 bv = src[kc * FV];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][q], bv, acc[q], 0, 0, 0);
+      for (int j = 0; j < NJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][j], bv, acc[i][j], 0, 0, 0);
+    }
+  };
+  // acc[i] += h_{t-1} W_hh^T, the h fragments read from LDS four K-chunks ahead of their MFMAs.
+  auto rec_mfma = [&](int i, const f16x8* hprev) {
+    constexpr int kAhead = 4;
+    f16x8 bq[kAhead];
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) bq[k] = hprev[k * FV + lane];
+#pragma unroll
+    for (int kc = 0; kc < KCH; ++kc) {
+      const f16x8 bv = bq[kc % kAhead];
+      if (kc + kAhead < KCH) bq[kc % kAhead] = hprev[(kc + kAhead) * FV + lane];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[KCH + kc][j], bv, acc[i][j], 0, 0, 0);
+    }
+  };
+  // Cell update of tile i, step t: element q of acc[i][j] is gate q of unit eu + 4 j.  Both units'
+  // updates are computed on every lane and then selected (under a branch on `live` the compiler
+  // would serialise the units' dependency chains).
+  auto cell = [&](int i, int t) {
+    const bool live = t < len[i];
+    float cn[NJ], hn[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      cn[j] = c[i][j];
+      lstm_cell(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3], cn[j], hn[j]);
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) part[pslot(i, t)][wave][q][lane] = acc[q];
+    for (int j = 0; j < NJ; ++j) asm volatile("" : "+v"(cn[j]), "+v"(hn[j]));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      c[i][j] = live ? cn[j] : c[i][j];
+      hcur[i][j] = live ? (_Float16)hn[j] : hcur[i][j];
+    }
   };
 
-  // Ring accesses.  Two-tile workgroups run out of VGPRs with global atomics, which hold a 64-bit
-  // VGPR address per word; they use buffer loads and stores instead: a descriptor of one ring slot
-  // (uniform, in SGPRs), the thread's byte offset in a VGPR and the word's block offset as the
-  // scalar offset, with cache policy sc1 (agent-scope coherent, as agent-scope relaxed atomics).
-  // Every offset stays inside the slot.  One-tile workgroups keep the global atomics: the extra
-  // SGPR pressure of the descriptors costs them more than the VGPRs save.  Descriptor word 3 is
-  // 0x00020000: DATA_FORMAT = 32 bit, which untyped buffer accesses need to be non-zero on CDNA.
-  auto ring_rs = [&](int i, int t) {
-    return __builtin_amdgcn_make_buffer_rsrc(xr(i) + (size_t)(t & 1) * C::kWords, 0, C::kWords * 8, 0x00020000);
+  // ---- exchange ----
+  // Ring of tile i: two slots of C::kWords words (PW used), slot t & 1 for step t; words in writer
+  // order [slice][wave][16 NJ]: lane (kgx, en) with kgx % KW == 0 writes word
+  // wave * 16 NJ + (kgx / KW) * 16 + en of its slice's block, carrying units (eu, eu + 1) and
+  // (eu + 4, eu + 5) (NJ = 2, from itself and lane + 16) or eu .. eu + 3 (NJ = 1, from lanes + 16,
+  // + 32, + 48) of row en.
+  auto xr = [&](int i) -> uint64_t* { return a.xring + ((size_t)layer * a.ntile + tile0 + i) * 2 * C::kWords; };
+  const int pwoff = slice * SB + wave * 16 * NJ + (kgx / KW) * 16 + en;
+  auto slot_rs = [&](int i, int t) {
+    return __builtin_amdgcn_make_buffer_rsrc(xr(i) + (size_t)__builtin_amdgcn_readfirstlane(t & 1) * C::kWords, 0,
+                                             PW * 8, 0x00020000);
   };
-  auto gload = [&](int i, int t, int r) -> uint64_t {
-    if constexpr (NTI == 2) {
-      return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(ring_rs(i, t), threadIdx.x * 8u, r * NT * 8, 16));
-    } else {
-      return load_agent_u64(xr(i) + (size_t)(t & 1) * C::kWords + threadIdx.x + r * NT);
-    }
+  // LDS destination (u32 index into a fragment-ordered h block) of the first pair of word m of a
+  // step; the second pair is D2 further.
+  auto word_dst = [](int m) -> int {
+    const int sl = m / SB, wq = m % SB;
+    const int wv_ = wq / (16 * NJ), rem = wq % (16 * NJ);
+    const int u0 = sl * HS + wv_ * UPW + (rem / 16) * KW;
+    return ((u0 >> 3) * 16 + (rem & 15)) * 4 + ((u0 & 7) >> 1);
   };
-  // Gather words of tile i, step t: issued right after the tile's own words are stored.
-  uint64_t wv[NTI][NW];
-  auto issue_gather = [&](int i, int t) {
+  int gdst[2 * NLD];
 #pragma unroll
-    for (int r = 0; r < NW; ++r) wv[i][r] = gload(i, t, r);
+  for (int r = 0; r < 2 * NLD; ++r) gdst[r] = word_dst(2 * ((int)threadIdx.x + (r >> 1) * NT) + (r & 1));
+  uint64_t wv[NTI][2 * NLD];
+  // Poll p of tile i, step t: words 2 (tid + p NT) and + 1 of the slot, one 16-byte load with sc1
+  // (each word is written by one aligned 8-byte store and lies inside the load, so it is read whole;
+  // its own tag validates it).
+  auto poll = [&](int i, int t, int p) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(slot_rs(i, t), threadIdx.x * 16u, p * NT * 16, 16);
+    wv[i][2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+    wv[i][2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
   };
-  // Complete the gather of tile i, step t, into hbuf[i]: re-poll the words whose tag is not t + 1
-  // yet.  Before spinning, the input waves compute tile i's partials for step t + 1 (ring slot
-  // s_next; -1: none).  False (uniformly) if any wait of the workgroup failed.
-  auto complete_gather = [&](int i, int t, int s_next) -> bool {
-    if (!recurrent && s_next >= 0) partials(i, t + 1, s_next);
-    const uint32_t want = (uint32_t)t + 1u;
+  uint32_t raw[NTI][2];  // h_t of the word this lane sends (writers): two pairs of fp16
+  // Tile i's h_t to the siblings: one word from each writer lane (the others address no word).
+  auto send = [&](int i, int t) {
+    uint32_t lo, hi;
+    if constexpr (NJ == 2) {
+      const uint32_t mine = (uint32_t)__builtin_bit_cast(uint16_t, hcur[i][0]) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, hcur[i][1]) << 16);
+      const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
+      lo = __builtin_amdgcn_perm(other, mine, 0x05040100u);
+      hi = __builtin_amdgcn_perm(other, mine, 0x07060302u);
+    } else {
+      const uint32_t mine = (uint32_t)__builtin_bit_cast(uint16_t, hcur[i][0]);
+      const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
+      lo = __builtin_amdgcn_perm(other, mine, 0x05040100u);
+      hi = (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, (int)lo);             // lane + 32's pair
+    }
+    raw[i][0] = lo;
+    raw[i][1] = hi;
+    const uint64_t word = (uint64_t)xw_enc_pair(lo) | ((uint64_t)xw_enc_pair(hi) << 32) | xw_tag_bits(xw_step_tag(t));
+    const auto wd = __builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, word);
+    const uint32_t woff = writer ? (uint32_t)pwoff * 8u : kOutOfRange;
+    // XCD-local groups store without sc1 (the word stays in their L2), others with it.
+    if (l2)
+      __builtin_amdgcn_raw_buffer_store_b64(wd, slot_rs(i, t), woff, 0, 1);
+    else
+      __builtin_amdgcn_raw_buffer_store_b64(wd, slot_rs(i, t), woff, 0, 16);
+  };
+  // The polls of tile i's step t, issued late in the phase (after the input part), when the
+  // siblings' words are usually written: a poll that finds a stale word costs a round trip at the
+  // gather.  Loads and stores retire in issue order, so the gather's wait covers nothing issued
+  // after these loads.
+  auto issue_poll = [&](int i, int t) {
+#pragma unroll
+    for (int p = 0; p < NLD; ++p) poll(i, t, p);
+  };
+  // Complete the gather of tile i, step t, into dst: re-poll the words whose tag is not step t's
+  // yet (bounded wait; a failure sets s_fail), then scatter them into fragment order.
+  auto gather = [&](int i, int t, f16x8* dst) {
+    const uint32_t want = xw_step_tag(t);
     uint64_t t0 = 0;
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < NW; ++r) ready = ready && word_tag(wv[i][r]) == want;
+      for (int r = 0; r < 2 * NLD; ++r) ready = ready && xw_tag(wv[i][r]) == want;
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -317,94 +409,67 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
           break;
         }
       }
-      if constexpr (NTI == 2) asm volatile("" ::: "memory");  // the buffer loads re-read the ring every spin
+      asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
-      for (int r = 0; r < NW; ++r)
-        if (word_tag(wv[i][r]) != want) wv[i][r] = gload(i, t, r);
+      for (int p = 0; p < NLD; ++p)
+        if (xw_tag(wv[i][2 * p]) != want || xw_tag(wv[i][2 * p + 1]) != want) poll(i, t, p);
     }
-    uint32_t* hb32 = reinterpret_cast<uint32_t*>(hbuf[i]);
+    // Every poll is followed by the same kAfterPoll operations before its gather, so this wait is
+    // implied by the poll's: it tells the compiler that everything issued before the poll is
+    // complete, which it cannot see across the loop.
+    __builtin_amdgcn_s_waitcnt(0x0F70 | kAfterPoll);
+    uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
 #pragma unroll
-    for (int r = 0; r < NW; ++r) hb32[gdst(r)] = (uint32_t)wv[i][r];
-    lds_barrier();
-    return s_fail == 0;
+    for (int r = 0; r < 2 * NLD; ++r) {
+      d32[gdst[r]] = xw_dec_pair((uint32_t)wv[i][r]);
+      d32[gdst[r] + D2] = xw_dec_pair((uint32_t)(wv[i][r] >> 32));
+    }
+  };
+  // The loads of this wave's previous phase of tile i (input piece, counter) were issued before the poll it
+  // has just waited for, so they are complete: the empty asm tells the compiler, which would
+  // otherwise wait for them as loads in flight where they are read.
+  auto settle = [&](int i) {
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) asm volatile("" : "+v"(pc[i][b]));
+    asm volatile("" : "+v"(cup[i]));
   };
 
-  // Gate math of tile i, step t, from the group's partial sums plus the bias.
-  auto gate_math = [&](int i, int t) {
-    const bool live = t < len[i];
-    if (!active) return;
-    float z[4][2];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float2 bv = s_bias[q][(eu - slice * HS) >> 1];
-      z[q][0] = bv.x;
-      z[q][1] = bv.y;
-#pragma unroll
-      for (int e = 0; e < WPG; ++e) {
-        const float2 v = reinterpret_cast<const float2*>(&part[pslot(i, t)][C::wave_of(g, e)][q][pl])[pp];
-        z[q][0] += v.x;
-        z[q][1] += v.y;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float cn = c[i][j], hn;
-      lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn, hn);
-      c[i][j] = live ? cn : c[i][j];
-      hcur[i][j] = live ? (_Float16)hn : hcur[i][j];
+  // Hand-off of tile i's h_t to the next layer (fragment order, sc1), from the writer lanes; the
+  // last layer's stores address an empty range (dropped).
+  const int hoff = ((eu >> 3) * 16 + en) * 8 + (eu & 7);  // halfs: (row en, unit eu) in a step block
+  auto handoff = [&](int i, int t) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        a.hseq + (((size_t)layer * a.ntile + tile0 + i) * a.T + t) * hstep, 0, has_down ? (int)(hstep * 16) : 0,
+        0x00020000);
+    const uint32_t off = writer ? (uint32_t)hoff * 2u : kOutOfRange;
+    if constexpr (NJ == 2) {
+      __builtin_amdgcn_raw_buffer_store_b32(raw[i][0], rs, off, 0, 16);
+      __builtin_amdgcn_raw_buffer_store_b32(raw[i][1], rs, off + 8u, 0, 16);
+    } else {
+      const __attribute__((ext_vector_type(2))) unsigned int v2 = {raw[i][0], raw[i][1]};
+      __builtin_amdgcn_raw_buffer_store_b64(v2, rs, off, 0, 16);
     }
   };
-  // Stores of tile i, step t: the tagged words, the hand-off and the output sequence.
-  auto store_h = [&](int i, int t) {
-    if (!active) return;
+  // The last layer's output sequence (issued before the step's ring poll, as it is optional).
+  auto store_out_seq = [&](int i, int t) {
+    if (has_down || !a.out_seq || !row_ok[i]) return;
     const bool live = t < len[i];
-    const uint64_t word = tag_word(hcur[i][0], hcur[i][1], (uint32_t)t + 1u);
-    // XCD-local groups store the word without sc1 (it stays in their L2), others with it.
-    if constexpr (NTI == 2) {
-      const auto wd = __builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, word);
-      if (l2)
-        __builtin_amdgcn_raw_buffer_store_b64(wd, ring_rs(i, t), (uint32_t)woff * 8u, 0, 1);
-      else
-        __builtin_amdgcn_raw_buffer_store_b64(wd, ring_rs(i, t), (uint32_t)woff * 8u, 0, 16);
-    } else {
-      if (l2)
-        __hip_atomic_store(xr(i) + (size_t)(t & 1) * C::kWords + woff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      else
-        __hip_atomic_store(xr(i) + (size_t)(t & 1) * C::kWords + woff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (has_down) {
-      union { _Float16 h[2]; uint32_t u; } v;
-      v.h[0] = hcur[i][0];
-      v.h[1] = hcur[i][1];
-      if constexpr (NTI == 2) {
-        const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc(my_seq(i) + (size_t)t * hstep, 0, (int)(hstep * 16), 0x00020000);
-        __builtin_amdgcn_raw_buffer_store_b32(v.u, rs, (uint32_t)hoff * 2u, 0, 16);
-      } else {
-        __hip_atomic_store(reinterpret_cast<uint32_t*>(reinterpret_cast<_Float16*>(my_seq(i) + (size_t)t * hstep) + hoff),
-                           v.u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    if (!has_down && a.out_seq && row_ok[i]) {
-      _Float16* dst = a.out_seq + ((size_t)grow[i] * a.T + t) * a.H + eu;
+    _Float16* dst = a.out_seq + ((size_t)grow[i] * a.T + t) * a.H + eu;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        if (eu + j < a.H) dst[j] = live ? hcur[i][j] : (_Float16)0.0f;
-    }
+    for (int j = 0; j < NJ; ++j)
+      if (eu + 4 * j < a.H) dst[4 * j] = live ? hcur[i][j] : (_Float16)0.0f;
   };
 
   int probe_i = 0;
-  // Probe steps live in SGPRs (see the wavefront kernel): a VGPR loaded in the loop would put a
-  // vmcnt(0) on every step.
+  // Probe steps live in SGPRs (a VGPR loaded in the loop would put a vmcnt(0) on every step).
   int probe_next = a.n_probe > 0 ? __builtin_amdgcn_readfirstlane(a.probe_steps[0]) : -1;
   auto write_probe = [&](int pi) {
-    if (!active) return;
 #pragma unroll
     for (int i = 0; i < NTI; ++i) {
       if (!row_ok[i]) continue;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int u = eu + j;
+      for (int j = 0; j < NJ; ++j) {
+        const int u = eu + 4 * j;
         if (u < a.H) {
           const size_t o = (((size_t)pi * a.L + layer) * a.B + grow[i]) * a.H + u;
           a.probe_h[o] = (float)hcur[i][j];
@@ -413,110 +478,152 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       }
     }
   };
-  // Hand-off stores complete, then count `steps` more steps of every tile of this workgroup.
-  auto publish = [&](uint32_t steps) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x < NTI) __hip_atomic_fetch_add(my_ctr(threadIdx.x), steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
 
-  for (int idx = threadIdx.x; idx < NTI * CH * KCH * FV; idx += NT) ring[idx / (CH * KCH * FV)][idx % (CH * KCH * FV)] = f16x8{};
-  __syncthreads();
-
+  // ---- prologue: inputs of steps 0 and 1 into the ring, step 2 into the piece registers, the
+  // upstream counter, and the first step's input part ----
   bool ok = __builtin_amdgcn_readfirstlane(s_fail) == 0;
   if (ok && Tt > 0) {
-    if (has_up) ok = acquire_up(0);
-    if (ok) {
-      load_chunk(0);
-      store_chunk(0);
-    }
-    if (ok && nchunk > 1) {
-      if (has_up) ok = acquire_up(1);
-      if (ok) load_chunk(1);
-    }
-  }
-  __syncthreads();
-
-  uint32_t unpublished = 0;  // steps computed since the last publication
-  // Two-tile workgroups: the upstream polls before the loop load into VGPRs that the compiler
-  // otherwise treats as possibly outstanding at the loop head, which put a vmcnt(0) (waiting for
-  // the other tile's gather) in front of every tile-step's MFMAs.  One wait here costs the first
-  // chunk's prefetch once (measured: C3 6.2 -> 5.7 ms; with one tile it is 2% slower, so only
-  // two-tile workgroups take it).
-  if constexpr (NTI == 2) __builtin_amdgcn_s_waitcnt(0);
-  for (int k = 0; ok && k < nchunk; ++k) {
-    if (k > 0) {
-      if (has_down && k % PUB == 0) {
-        publish(unpublished);
-        unpublished = 0;
-      } else {
-        __syncthreads();
-      }
-      store_chunk(k);
-      const bool more = k + 1 < nchunk;
-      if (has_up && more) {
-        if (!acquire_up(k + 1)) {
-          ok = false;
-          break;
-        }
-      } else {
-        __syncthreads();
-      }
-      if (more) load_chunk(k + 1);
-    }
-    const int ns = min(CH, Tt - k * CH);
-    for (int s = 0; s < ns && ok; ++s) {
-      const int t = k * CH + s;
-      if constexpr (NTI == 1) {
-        // h_{t-1} (the input partials for step t are computed while the words arrive).
-        if (t > 0 && !complete_gather(0, t - 1, s)) {
-          ok = false;
-          break;
-        }
-        if (t == 0 || recurrent) partials(0, t, s);
-        lds_barrier();
-        gate_math(0, t);
-        store_h(0, t);
-        issue_gather(0, t);
-      } else {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          partials(i, t, s);
-          lds_barrier();
-          gate_math(i, t);
-          // The other tile's gather: tile 1's of step t-1 (for tile 0), tile 0's of step t (for tile 1).
-          const int to = i == 0 ? t - 1 : t;
-          if (to >= 0 && !complete_gather(1 - i, to, -1)) {
-            ok = false;
-            break;
-          }
-          store_h(i, t);
-          issue_gather(i, t);
-        }
-        if (!ok) break;
+    for (int i = 0; i < NTI; ++i) {
+      if (has_up && !need_input(i, clamp_step(D - 1))) ok = false;
+      if (!ok) break;
+#pragma unroll
+      for (int s = 0; s < D - 1; ++s) {
+        load_piece(i, clamp_step(s));
+        wait_vmem_all();
+        store_piece(i, s);
       }
-      if (t + 1 == probe_next) {
-        write_probe(probe_i);
-        ++probe_i;
-        probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
-      }
-      ++unpublished;
+      load_piece(i, clamp_step(D - 1));
+      load_counter(i);
+    }
+    if (!ok) s_fail = 1;
+  }
+  wait_vmem_all();
+  __syncthreads();
+  ok = __builtin_amdgcn_readfirstlane(s_fail) == 0;
+  if (ok && Tt > 0) {
+#pragma unroll
+    for (int i = 0; i < NTI; ++i) input_mfma(i, 0);
+  }
+  lds_barrier();  // step 0 overwrites ring slot 0 (with x_2) once every wave has read x_0
+
+  // ---- steps ----
+  // Phase (i, t) of a two-tile workgroup: h_{t-1} W_hh^T and the cell update of tile i; the other
+  // tile's gather (tile 1's of step t - 1 for tile 0, tile 0's of step t for tile 1); tile i's
+  // input of step t + 2 into the ring; tile i's word and hand-off stores; x_{t+1} W_ih^T; the polls
+  // of step t, then the input piece of step t + 3 and the counter; one barrier, after which thread 0
+  // publishes.  One tile: the tile's own polls, hand-off and gather follow its input part,
+  // into the other h buffer.  Probes are written once both tiles have completed a step.
+  // The phases after the cell update and gather: ring input, word, input part, polls, hand-off,
+  // next input piece and counter, barrier, publication.  False if a wait of the workgroup failed.
+  auto finish_phase = [&](int i, int t) -> bool {
+    if constexpr (NTI == 2) {
+      settle(i);
+      store_piece(i, t + 2);
+      send(i, t);
+      handoff(i, t);
+      if (threadIdx.x == 0) s_up[i] = cup[i];
+      if (has_up && !need_input(i, clamp_step(t + D))) s_fail = 1;
+      if (t + 1 < Tt) input_mfma(i, t + 1);
+      issue_poll(i, t);
+    } else {
+      send(0, t);
+      if (t + 1 < Tt) input_mfma(0, t + 1);
+      issue_poll(0, t);
+      handoff(0, t);
+      gather(0, t, hbuf[(t + 1) & 1]);
+      settle(0);
+      store_piece(0, t + 2);
+      if (threadIdx.x == 0) s_up[0] = cup[0];
+      if (has_up && !need_input(0, clamp_step(t + D))) s_fail = 1;
+    }
+    // After the polls: the input piece D steps ahead (its upstream group is published) and the
+    // counter (with one tile, the hand-off stores as well).
+    load_piece(i, clamp_step(t + D));
+    load_counter(i);
+    lds_barrier();
+    if (has_down) publish(i, t);
+    return __builtin_amdgcn_readfirstlane(s_fail) == 0;
+  };
+  auto after_step = [&](int t) {
+    if (t + 1 == probe_next) {
+      write_probe(probe_i);
+      ++probe_i;
+      probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
+    }
+  };
+  if constexpr (NTI == 2) {
+    // Phase (0, 0) has no gather to complete; the loop runs phase (1, t), then (0, t + 1), each
+    // after the other tile's gather (so every phase in the loop has one).
+    if (ok && Tt > 0) {
+      rec_mfma(0, hbuf[0]);
+      cell(0, 0);
+      store_out_seq(0, 0);
+      ok = finish_phase(0, 0);
+    }
+    for (int t = 0; ok && t < Tt; ++t) {
+      rec_mfma(1, hbuf[1]);
+      cell(1, t);
+      store_out_seq(1, t);
+      gather(0, t, hbuf[0]);
+      if (!(ok = finish_phase(1, t))) break;
+      after_step(t);
+      if (t + 1 == Tt) break;
+      rec_mfma(0, hbuf[0]);
+      cell(0, t + 1);
+      store_out_seq(0, t + 1);
+      gather(1, t, hbuf[1]);
+      ok = finish_phase(0, t + 1);
+    }
+  } else {
+    for (int t = 0; ok && t < Tt; ++t) {
+      rec_mfma(0, hbuf[t & 1]);
+      cell(0, t);
+      store_out_seq(0, t);
+      if (!(ok = finish_phase(0, t))) break;
+      after_step(t);
     }
   }
-  // Final publication, and the final h of the tile whose last gather is still open (the other
-  // tile's completed during that tile's last step) for the head.
+  // The last gather of a two-tile workgroup (tile 1's last step) and the final publication, once
+  // every wave's hand-off stores are complete.
   if (ok && Tt > 0) {
-    if (has_down) publish(unpublished);
-    if (!complete_gather(NTI - 1, Tt - 1, -1)) ok = false;
+    if constexpr (NTI == 2) gather(1, Tt - 1, hbuf[1]);
+    wait_vmem_all();
+    __syncthreads();
+    ok = __builtin_amdgcn_readfirstlane(s_fail) == 0;
+    if (ok && has_down) {
+#pragma unroll
+      for (int i = 0; i < NTI; ++i) publish(i, Tt);
+    }
+  }
+  auto hfinal = [&](int i) -> f16x8* { return NTI == 2 ? hbuf[i] : hbuf[Tt & 1]; };
+  // Rows of length 0 keep their h0, which the packed exchange may not carry intact: restore their
+  // h in the final buffer before the head reads it.
+  if (ok && a.lengths && Tt > 0) {
+#pragma unroll
+    for (int i = 0; i < NTI; ++i) {
+      for (int idx = threadIdx.x; idx < KCH * FV; idx += NT) {
+        const int kc = idx / FV, l = idx % FV;
+        const int gr = a.row0 + (tile0 + i) * 16 + (l & 15);
+        if (gr >= a.row_end || a.lengths[gr] > 0) continue;
+        const int k0 = kc * 32 + (l >> 4) * 8;
+        f16x8 v = {};
+        if (a.h0) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (k0 + j < a.H) v[j] = a.h0[((size_t)layer * a.B + gr) * a.H + k0 + j];
+        }
+        hfinal(i)[idx] = v;
+      }
+    }
+    __syncthreads();
   }
 
   if (!ok) {
     // A wait failed: poison every output of this workgroup (states, probes, output sequence, head).
-    if (active) {
 #pragma unroll
-      for (int i = 0; i < NTI; ++i)
-        if (row_ok[i]) poison_lane_outputs(a, layer, grow[i], eu, 2, !has_down);
-    }
+    for (int i = 0; i < NTI; ++i)
+      if (row_ok[i]) poison_lane_outputs(a, layer, grow[i], eu, NJ, !has_down, 4);
     if (!has_down && slice == 0 && a.out) {
       for (int idx = threadIdx.x; idx < NTI * 16 * a.O; idx += NT) {
         const int gr = a.row0 + tile0 * 16 + idx / a.O;
@@ -526,15 +633,16 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     return;
   }
 
-  if (!has_down && a.out_seq && active) {
+  // Steps past the workgroup's longest row were never visited: their output sequence is zero.
+  if (!has_down && a.out_seq) {
 #pragma unroll
     for (int i = 0; i < NTI; ++i) {
       if (!row_ok[i]) continue;
       for (int t = Tt; t < a.T; ++t) {
         _Float16* dst = a.out_seq + ((size_t)grow[i] * a.T + t) * a.H + eu;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          if (eu + j < a.H) dst[j] = (_Float16)0.0f;
+        for (int j = 0; j < NJ; ++j)
+          if (eu + 4 * j < a.H) dst[4 * j] = (_Float16)0.0f;
       }
     }
   }
@@ -542,29 +650,27 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     write_probe(probe_i);
     ++probe_i;
   }
-  if (active) {
 #pragma unroll
-    for (int i = 0; i < NTI; ++i) {
-      if (!row_ok[i]) continue;
+  for (int i = 0; i < NTI; ++i) {
+    if (!row_ok[i]) continue;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int u = eu + j;
-        if (u < a.H) {
-          const size_t si = ((size_t)layer * a.B + grow[i]) * a.H + u;
-          if (a.h_n) a.h_n[si] = hcur[i][j];
-          if (a.c_n) a.c_n[si] = (_Float16)c[i][j];
-        }
+    for (int j = 0; j < NJ; ++j) {
+      const int u = eu + 4 * j;
+      if (u < a.H) {
+        const size_t si = ((size_t)layer * a.B + grow[i]) * a.H + u;
+        if (a.h_n) a.h_n[si] = hcur[i][j];
+        if (a.c_n) a.c_n[si] = (_Float16)c[i][j];
       }
     }
   }
-  // Linear head (last layer, first slice) on the full final h held in hbuf.
+  // Linear head (last layer, first slice) on the full final h.
   if (!has_down && slice == 0 && a.out) {
     for (int idx = threadIdx.x; idx < NTI * 16 * a.O; idx += NT) {
       const int rt = idx / a.O, o = idx % a.O;
       const int i = rt / 16, rr = rt % 16;
       const int gr = a.row0 + (tile0 + i) * 16 + rr;
       if (gr >= a.row_end) continue;
-      const _Float16* hf = reinterpret_cast<const _Float16*>(hbuf[i]);
+      const _Float16* hf = reinterpret_cast<const _Float16*>(hfinal(i));
       const float* wr = a.wlin + (size_t)o * HP;
       float s0 = 0.f, s1 = 0.f;
       for (int k8 = 0; k8 < HP; k8 += 8) {
@@ -582,18 +688,12 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 
 }  // namespace
 
-// Steps per chunk of the sliced kernels: the input ring holds wg_tiles * CH * HP / 32 fragment
-// blocks and each thread stages its share of one chunk in VGPRs.
-constexpr int kChunk256 = 4;
-constexpr int kChunk256x2 = 2;
-constexpr int kChunk512 = 2;
-
 const void* sliced_kernel(int HP, int wg_tiles) {
   switch (HP) {
     case 256:
-      return wg_tiles == 2 ? reinterpret_cast<const void*>(&lstm_sliced_kernel<256, kChunk256x2, 2>)
-                           : reinterpret_cast<const void*>(&lstm_sliced_kernel<256, kChunk256, 1>);
-    case 512: return wg_tiles == 1 ? reinterpret_cast<const void*>(&lstm_sliced_kernel<512, kChunk512, 1>) : nullptr;
+      return wg_tiles == 2 ? reinterpret_cast<const void*>(&lstm_sliced_kernel<256, 2>)
+                           : reinterpret_cast<const void*>(&lstm_sliced_kernel<256, 1>);
+    case 512: return wg_tiles == 1 ? reinterpret_cast<const void*>(&lstm_sliced_kernel<512, 1>) : nullptr;
     default: return nullptr;
   }
 }

@@ -97,7 +97,8 @@ def test_sliced_workspace_layout(ext):
     # H > 128: the hidden units of a layer are split over several workgroups ("slices").  The workspace
     # holds the (L-1)-layer hand-off plus a two-step ring of tagged words per (layer, tile) through which
     # the slices exchange h every step: L * tiles * 2 * (HP * 8) words of 8 bytes, and 8 more words per
-    # (layer, tile) for the slices' XCD ids.  Without a device the
+    # (layer, tile) for the slices' XCD ids; each (layer, tile) progress counter has a 128-byte line
+    # of its own.  Without a device the
     # plan assumes 256 co-resident workgroups: 256 / (L * 4 slices) = 16 workgroups per layer at
     # HP = 256, each carrying two 16-row tiles (the whole 512-row batch), and 256 / (L * 16) = 4
     # one-tile workgroups at HP = 512 (a 64-row batch: one launch, where the wavefront path is the
@@ -109,7 +110,8 @@ def test_sliced_workspace_layout(ext):
         handoff = (L - 1) * rows * T * H * 2
         ring = L * tiles * (2 * H * 8 + 8) * 8  # + a table of up to 16 slices' XCD ids per (layer, tile)
         xp = rows * T * 8 * 2  # x of the launch: one 8-wide K group (I = 5) per row and step
-        assert handoff + ring + xp <= b < handoff + ring + xp + (1 << 12)
+        counters = L * tiles * 128  # one 128-byte line per (layer, tile)
+        assert handoff + ring + xp + counters <= b < handoff + ring + xp + counters + (1 << 12)
 
 
 def test_layer_sequential_workspace_layout(ext):
@@ -137,7 +139,7 @@ def test_layer_sequential_workspace_layout(ext):
     # x, the (L-1)-layer hand-off and the ring), whatever the batch
     T = 10000
     b = ext.workspace_bytes(5, H, L, 24, 512, T)
-    wave = 64 * T * 8 * 2 + (L - 1) * 64 * T * H * 2 + L * 4 * (2 * H * 8 + 8) * 8
+    wave = 64 * T * 8 * 2 + (L - 1) * 64 * T * H * 2 + L * 4 * (2 * H * 8 + 8) * 8 + L * 4 * 128
     assert wave <= b < wave + (1 << 12)
 
 

@@ -53,9 +53,9 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   constexpr int G = 2;                    // steps per publication of the hand-off
   constexpr int D = 3;                    // steps between an input's load and its use
   constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every range: stores dropped
-  // Memory operations issued after a poll before its gather: with two tiles the input pieces and
-  // the counter load, with one the hand-off stores.
-  constexpr int kAfterPoll = NTI == 2 ? BPW + 1 : (NJ == 2 ? 2 : 1);
+  // Memory operations issued after a poll before its gather: with one tile the hand-off stores,
+  // with two none.
+  constexpr int kAfterPoll = NTI == 2 ? 0 : (NJ == 2 ? 2 : 1);
   static_assert(kAfterPoll < 16, "vmcnt field");
   static_assert(NTI == 1 || NTI == 2, "one or two tiles per workgroup");
   static_assert(PW % (2 * NT) == 0 && KCH % 8 == 0, "whole loads per thread");
@@ -174,10 +174,9 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     for (int j = 0; j < NJ; ++j) bias[q][j] = s_bias[q][wave * UPW + kgx + 4 * j];
 
   // ---- layer input: staged into the LDS ring in 1 KB pieces, D steps ahead ----
-  // Every phase issues the same memory operations after its ring poll on every path (the
-  // hand-off stores, BPW piece loads and one counter load; lanes and layers without a use for one
-  // address it out of range or at a dummy word), so the next poll's wait counts them exactly and
-  // waits for the poll alone, not for the slower loads issued after it.
+  // Every phase issues the same memory operations on every path (the hand-off stores, BPW piece
+  // loads and one counter load; lanes and layers without a use for one address it out of range or
+  // at a dummy word), so the compiler can count exactly what a poll's wait covers.
   const int per = has_up ? KCH * FV : a.g_in0 * 16;  // f16x8 per step in the source
   const size_t hstep = (size_t)KCH * FV;
   // Descriptor of tile i's input of step s (word 3 0x00020000: DATA_FORMAT = 32 bit, which untyped
@@ -342,14 +341,16 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   int gdst[2 * NLD];
 #pragma unroll
   for (int r = 0; r < 2 * NLD; ++r) gdst[r] = word_dst(2 * ((int)threadIdx.x + (r >> 1) * NT) + (r & 1));
-  uint64_t wv[NTI][2 * NLD];
+  // Poll results: one set for both tiles (a tile's polls are issued at the end of its phase and
+  // gathered in the next phase, before the other tile's polls are issued).
+  uint64_t wv[2 * NLD];
   // Poll p of tile i, step t: words 2 (tid + p NT) and + 1 of the slot, one 16-byte load with sc1
   // (each word is written by one aligned 8-byte store and lies inside the load, so it is read whole;
   // its own tag validates it).
   auto poll = [&](int i, int t, int p) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(slot_rs(i, t), threadIdx.x * 16u, p * NT * 16, 16);
-    wv[i][2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
-    wv[i][2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
+    wv[2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+    wv[2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
   };
   uint32_t raw[NTI][2];  // h_t of the word this lane sends (writers): two pairs of fp16
   // Tile i's h_t to the siblings: one word from each writer lane (the others address no word).
@@ -394,7 +395,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < 2 * NLD; ++r) ready = ready && xw_tag(wv[i][r]) == want;
+      for (int r = 0; r < 2 * NLD; ++r) ready = ready && xw_tag(wv[r]) == want;
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -412,7 +413,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
       for (int p = 0; p < NLD; ++p)
-        if (xw_tag(wv[i][2 * p]) != want || xw_tag(wv[i][2 * p + 1]) != want) poll(i, t, p);
+        if (xw_tag(wv[2 * p]) != want || xw_tag(wv[2 * p + 1]) != want) poll(i, t, p);
     }
     // Every poll is followed by the same kAfterPoll operations before its gather, so this wait is
     // implied by the poll's: it tells the compiler that everything issued before the poll is
@@ -421,8 +422,8 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
 #pragma unroll
     for (int r = 0; r < 2 * NLD; ++r) {
-      d32[gdst[r]] = xw_dec_pair((uint32_t)wv[i][r]);
-      d32[gdst[r] + D2] = xw_dec_pair((uint32_t)(wv[i][r] >> 32));
+      d32[gdst[r]] = xw_dec_pair((uint32_t)wv[r]);
+      d32[gdst[r] + D2] = xw_dec_pair((uint32_t)(wv[r] >> 32));
     }
   };
   // The loads of this wave's previous phase of tile i (input piece, counter) were issued before the poll it
@@ -510,23 +511,30 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   // ---- steps ----
   // Phase (i, t) of a two-tile workgroup: h_{t-1} W_hh^T and the cell update of tile i; the other
   // tile's gather (tile 1's of step t - 1 for tile 0, tile 0's of step t for tile 1); tile i's
-  // input of step t + 2 into the ring; tile i's word and hand-off stores; x_{t+1} W_ih^T; the polls
-  // of step t, then the input piece of step t + 3 and the counter; one barrier, after which thread 0
+  // input of step t + 2 into the ring; tile i's word and hand-off stores; the input piece of step
+  // t + 3 and the counter; x_{t+1} W_ih^T; the polls of step t; one barrier, after which thread 0
   // publishes.  One tile: the tile's own polls, hand-off and gather follow its input part,
   // into the other h buffer.  Probes are written once both tiles have completed a step.
   // The phases after the cell update and gather: ring input, word, input part, polls, hand-off,
   // next input piece and counter, barrier, publication.  False if a wait of the workgroup failed.
   auto finish_phase = [&](int i, int t) -> bool {
     if constexpr (NTI == 2) {
+      // The polls go last: the next phase's gather waits for them alone, and the input piece and
+      // counter (issued before the input part) have the time of the input part and of the polls'
+      // round trip to arrive.
       settle(i);
       store_piece(i, t + 2);
       send(i, t);
       handoff(i, t);
       if (threadIdx.x == 0) s_up[i] = cup[i];
       if (has_up && !need_input(i, clamp_step(t + D))) s_fail = 1;
+      load_piece(i, clamp_step(t + D));
+      load_counter(i);
       if (t + 1 < Tt) input_mfma(i, t + 1);
       issue_poll(i, t);
     } else {
+      // One tile gathers its own polls within the phase: the input piece and counter are issued
+      // after the gather, so that its wait does not include them.
       send(0, t);
       if (t + 1 < Tt) input_mfma(0, t + 1);
       issue_poll(0, t);
@@ -536,11 +544,9 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       store_piece(0, t + 2);
       if (threadIdx.x == 0) s_up[0] = cup[0];
       if (has_up && !need_input(0, clamp_step(t + D))) s_fail = 1;
+      load_piece(0, clamp_step(t + D));
+      load_counter(0);
     }
-    // After the polls: the input piece D steps ahead (its upstream group is published) and the
-    // counter (with one tile, the hand-off stores as well).
-    load_piece(i, clamp_step(t + D));
-    load_counter(i);
     lds_barrier();
     if (has_down) publish(i, t);
     return __builtin_amdgcn_readfirstlane(s_fail) == 0;

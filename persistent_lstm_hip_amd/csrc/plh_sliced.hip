@@ -53,10 +53,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   constexpr int G = 2;                    // steps per publication of the hand-off
   constexpr int D = 3;                    // steps between an input's load and its use
   constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every range: stores dropped
-  // Memory operations issued after a poll before its gather: with one tile the hand-off stores,
-  // with two none.
-  constexpr int kAfterPoll = NTI == 2 ? 0 : (NJ == 2 ? 2 : 1);
-  static_assert(kAfterPoll < 16, "vmcnt field");
   static_assert(NTI == 1 || NTI == 2, "one or two tiles per workgroup");
   static_assert(PW % (2 * NT) == 0 && KCH % 8 == 0, "whole loads per thread");
 
@@ -209,10 +205,8 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 
   // ---- hand-off publication and its check by the next layer ----
   // A (layer, tile) counter counts groups of G steps times the S slices: thread 0 of each slice
-  // adds a group once every wave of its workgroup has completed that group's hand-off stores.
-  // Wave 0 reads the upstream counter every phase of a tile (issued after the poll, used a phase
-  // of that tile later) and shares it in LDS; the other waves load a ring word nobody writes in
-  // its place.
+  // adds a group once its workgroup's hand-off stores of that group are complete.  Wave 0 reads the
+  // upstream counter every phase of a tile (used a phase of that tile later) and shares it in LDS.
   constexpr int CS = kSlicedCounterStride;
   auto up_ctr = [&](int i) -> uint32_t* { return a.counters + ((size_t)(layer - 1) * a.ntile + tile0 + i) * CS; };
   auto my_ctr = [&](int i) -> uint32_t* { return a.counters + ((size_t)layer * a.ntile + tile0 + i) * CS; };
@@ -228,16 +222,12 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     if (threadIdx.x == 0) s_up[i] = 0;
   }
   auto load_counter = [&](int i) {
-    const uint32_t* p = (has_up && wave == 0)
-                            ? up_ctr(i)
-                            : reinterpret_cast<const uint32_t*>(a.xring + ((size_t)layer * a.ntile + tile0 + i) * 2 * C::kWords +
-                                                                C::kWords + PW + wave * 16);
-    cup[i] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (has_up && wave == 0) cup[i] = __hip_atomic_load(up_ctr(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  // Thread 0, after a phase's barrier: every wave has completed its hand-off stores of tile i's
-  // steps < t (issued before the poll it waited for in that phase).
-  auto publish = [&](int i, int t) {
-    const int groups = t >= Tt ? (Tt + G - 1) / G : t / G;
+  // Thread 0, after a phase's barrier: the hand-off stores of tile i's steps < n are complete (each
+  // was issued before a poll its wave has waited for).
+  auto publish = [&](int i, int n) {
+    const int groups = n >= Tt ? (Tt + G - 1) / G : n / G;
     if (groups > pub[i]) {
       if (threadIdx.x == 0)
         __hip_atomic_fetch_add(my_ctr(i), (uint32_t)(groups - pub[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -352,7 +342,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     wv[2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
     wv[2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
   };
-  uint32_t raw[NTI][2];  // h_t of the word this lane sends (writers): two pairs of fp16
   // Tile i's h_t to the siblings: one word from each writer lane (the others address no word).
   auto send = [&](int i, int t) {
     uint32_t lo, hi;
@@ -368,8 +357,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       lo = __builtin_amdgcn_perm(other, mine, 0x05040100u);
       hi = (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, (int)lo);             // lane + 32's pair
     }
-    raw[i][0] = lo;
-    raw[i][1] = hi;
     const uint64_t word = (uint64_t)xw_enc_pair(lo) | ((uint64_t)xw_enc_pair(hi) << 32) | xw_tag_bits(xw_step_tag(t));
     const auto wd = __builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, word);
     const uint32_t woff = writer ? (uint32_t)pwoff * 8u : kOutOfRange;
@@ -415,10 +402,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       for (int p = 0; p < NLD; ++p)
         if (xw_tag(wv[2 * p]) != want || xw_tag(wv[2 * p + 1]) != want) poll(i, t, p);
     }
-    // Every poll is followed by the same kAfterPoll operations before its gather, so this wait is
-    // implied by the poll's: it tells the compiler that everything issued before the poll is
-    // complete, which it cannot see across the loop.
-    __builtin_amdgcn_s_waitcnt(0x0F70 | kAfterPoll);
     uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
 #pragma unroll
     for (int r = 0; r < 2 * NLD; ++r) {
@@ -435,21 +418,17 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     asm volatile("" : "+v"(cup[i]));
   };
 
-  // Hand-off of tile i's h_t to the next layer (fragment order, sc1), from the writer lanes; the
-  // last layer's stores address an empty range (dropped).
-  const int hoff = ((eu >> 3) * 16 + en) * 8 + (eu & 7);  // halfs: (row en, unit eu) in a step block
-  auto handoff = [&](int i, int t) {
+  // Hand-off to the next layer: h_s of tile i, this slice's HS units, from its fragment-ordered h
+  // block to the hand-off buffer (the same order), one 16-byte sc1 store per thread of waves 0 ..
+  // HS / 32 - 1, a phase after the gather that completed it.
+  constexpr int CPY = HS / 32 * FV;  // f16x8 of a slice's units per step
+  auto copy_out = [&](int i, int s_, const f16x8* src) {
+    if (!has_down || (int)threadIdx.x >= CPY) return;
+    const int idx = slice * CPY + (int)threadIdx.x;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        a.hseq + (((size_t)layer * a.ntile + tile0 + i) * a.T + t) * hstep, 0, has_down ? (int)(hstep * 16) : 0,
-        0x00020000);
-    const uint32_t off = writer ? (uint32_t)hoff * 2u : kOutOfRange;
-    if constexpr (NJ == 2) {
-      __builtin_amdgcn_raw_buffer_store_b32(raw[i][0], rs, off, 0, 16);
-      __builtin_amdgcn_raw_buffer_store_b32(raw[i][1], rs, off + 8u, 0, 16);
-    } else {
-      const __attribute__((ext_vector_type(2))) unsigned int v2 = {raw[i][0], raw[i][1]};
-      __builtin_amdgcn_raw_buffer_store_b64(v2, rs, off, 0, 16);
-    }
+        a.hseq + (((size_t)layer * a.ntile + tile0 + i) * a.T + s_) * hstep, 0, (int)(hstep * 16), 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, src[idx]),
+                                           rs, (uint32_t)idx * 16u, 0, 16);
   };
   // The last layer's output sequence (issued before the step's ring poll, as it is optional).
   auto store_out_seq = [&](int i, int t) {
@@ -525,7 +504,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       settle(i);
       store_piece(i, t + 2);
       send(i, t);
-      handoff(i, t);
+      if (t > 0) copy_out(i, t - 1, hbuf[i]);
       if (threadIdx.x == 0) s_up[i] = cup[i];
       if (has_up && !need_input(i, clamp_step(t + D))) s_fail = 1;
       load_piece(i, clamp_step(t + D));
@@ -538,17 +517,17 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       send(0, t);
       if (t + 1 < Tt) input_mfma(0, t + 1);
       issue_poll(0, t);
-      handoff(0, t);
       gather(0, t, hbuf[(t + 1) & 1]);
       settle(0);
       store_piece(0, t + 2);
+      if (t > 0) copy_out(0, t - 1, hbuf[t & 1]);
       if (threadIdx.x == 0) s_up[0] = cup[0];
       if (has_up && !need_input(0, clamp_step(t + D))) s_fail = 1;
       load_piece(0, clamp_step(t + D));
       load_counter(0);
     }
     lds_barrier();
-    if (has_down) publish(i, t);
+    if (has_down) publish(i, t - 1);
     return __builtin_amdgcn_readfirstlane(s_fail) == 0;
   };
   auto after_step = [&](int t) {
@@ -593,7 +572,14 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   // The last gather of a two-tile workgroup (tile 1's last step) and the final publication, once
   // every wave's hand-off stores are complete.
   if (ok && Tt > 0) {
-    if constexpr (NTI == 2) gather(1, Tt - 1, hbuf[1]);
+    if constexpr (NTI == 2) {
+      gather(1, Tt - 1, hbuf[1]);
+      __syncthreads();
+      copy_out(0, Tt - 1, hbuf[0]);
+      copy_out(1, Tt - 1, hbuf[1]);
+    } else {
+      copy_out(0, Tt - 1, hbuf[Tt & 1]);
+    }
     wait_vmem_all();
     __syncthreads();
     ok = __builtin_amdgcn_readfirstlane(s_fail) == 0;

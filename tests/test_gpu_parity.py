@@ -371,13 +371,17 @@ def test_layer_sequential_short_sequences(gpu, T):
     assert_close(c.float().cpu().numpy(), want_c.numpy(), what=f"T={T} c_n")
 
 
-def test_layer_sequential_zero_lengths_large_state_and_nan(gpu):
-    """The layer-sequential exchange packs 4 fp16 per word with the step tag in bit 14 of each (clear
-    in every computed h).  Rows of length 0 keep h0, which may use that bit (|h0| >= 2 here): their
-    results must still be exact, and no wait may hang on a clobbered tag.  A NaN input row must give
-    NaN (NaN travels as a reserved code) and leave the other rows untouched."""
-    I, H, L, O, B, T = 5, 512, 2, 7, 600, 2  # 600 rows, 2 steps: the layer-sequential path's choice
-    _say("layer-sequential zero lengths, |h0| >= 2, NaN row")
+@pytest.mark.parametrize("H,B,T", [(512, 600, 2), (256, 600, 5), (256, 40, 5), (512, 200, 3)],
+                         ids=["layer-sequential", "sliced-two-tiles", "sliced-one-tile", "sliced-H512"])
+def test_packed_exchange_zero_lengths_large_state_and_nan(gpu, H, B, T):
+    """The layer-sequential and sliced exchanges pack 4 fp16 per word with the step tag in bit 14 of
+    each (clear in every computed h).  Rows of length 0 keep h0, which may use that bit (|h0| >= 2
+    here): their results must still be exact, and no wait may hang on a clobbered tag.  A NaN input
+    row must give NaN (NaN travels as a reserved code) and leave the other rows untouched.  At L = 2
+    the path follows from the batch: H512 with 600 rows runs layer by layer, H512 with 200 rows and
+    H256 run the sliced kernel (600 rows: two tiles per workgroup; 40 rows: one)."""
+    I, L, O = 5, 2, 7
+    _say(f"packed exchange zero lengths, |h0| >= 2, NaN row H={H} B={B} T={T}")
     device = torch.device("cuda")
     torch.manual_seed(51)
     lstm = torch.nn.LSTM(I, H, L, batch_first=True)
@@ -386,7 +390,7 @@ def test_layer_sequential_zero_lengths_large_state_and_nan(gpu):
     g = torch.Generator().manual_seed(53)
     lengths = torch.randint(0, T + 1, (B,), generator=g)
     lengths[:20] = 0
-    lengths[300:310] = 0
+    lengths[B // 2:B // 2 + 10] = 0
     h0 = (3.0 * torch.randn(L, B, H, generator=g)).half()
     c0 = (0.5 * torch.randn(L, B, H, generator=g)).half()
     params = [[getattr(lstm, f"{n}_l{l}").detach().cuda() for l in range(L)]
@@ -395,7 +399,7 @@ def test_layer_sequential_zero_lengths_large_state_and_nan(gpu):
     res = gpu.forward(packed, (I, H, L, O), x.to(device, torch.float16), lengths=lengths, h0=h0.to(device),
                       c0=c0.to(device), want_out=True, want_seq=True, want_state=True, probe_steps=[1, 2],
                       check_status=True)
-    rows = np.r_[0:40, 295:320, 560:600]
+    rows = np.unique(np.r_[0:min(40, B), B // 2 - 5:B // 2 + 20, max(0, B - 40):B])
     want = oracle.lstm_forward(x.numpy()[rows], oracle_layers(lstm), lengths=lengths.numpy()[rows],
                                h0=h0.float().numpy()[:, rows], c0=c0.float().numpy()[:, rows],
                                probe_steps=[1, 2], want_seq=True)

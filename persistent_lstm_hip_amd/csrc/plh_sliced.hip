@@ -9,7 +9,7 @@
 //     lane all four gates of its units eu + 4 j for one row, and the cell update needs no other
 //     wave: no partial sums cross waves;
 //   * a step's gate sums are one MFMA chain per tile that starts from the bias: the input part
-//     x_t W_ih^T is computed a phase ahead (off the critical path, from the layer input staged in
+//     x_t W_ih^T is computed a step ahead (off the critical path, from the layer input staged in
 //     LDS), and only h_{t-1} W_hh^T (KCH NJ MFMAs per wave) sits between a step's exchange and its
 //     cell update;
 //   * the slices exchange h_t every step through a two-slot ring of tagged 64-bit words (the xw_*
@@ -17,11 +17,12 @@
 //     words (its own included) until their tags are the step's, with no counter or barrier between
 //     a slice's cell update and its siblings' next step.  When the S slices of a group run on one
 //     XCD (checked at entry) the words are stored without sc1 and stay in its L2 (same_xcd_group);
-//   * with two tiles per workgroup (NTI = 2) the tiles alternate phases: a tile's exchange runs
-//     while the other tile computes, and one workgroup barrier per phase orders LDS;
+//   * with two tiles per workgroup (NTI = 2) a step computes both tiles, so its fixed costs (the
+//     exchange's round trip, the memory issue of eight waves, one workgroup barrier) are paid once
+//     per two tiles;
 //   * layers run as a wavefront.  h_t also goes to the hand-off buffer (hseq, fragment order, sc1
 //     stores); each wave publishes its stores per group of G steps with one atomic add to the
-//     (layer, tile) counter, and the next layer's waves check that counter (prefetched a phase
+//     (layer, tile) counter, and the next layer's waves check that counter (prefetched a step
 //     ahead) before they load an input step, D steps before it is used, in 1 KB pieces staged
 //     through registers into a two-slot LDS ring.
 //
@@ -56,9 +57,9 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   static_assert(NTI == 1 || NTI == 2, "one or two tiles per workgroup");
   static_assert(PW % (2 * NT) == 0 && KCH % 8 == 0, "whole loads per thread");
 
-  // h_{t-1} in fragment order: per tile with two tiles (a tile's h is gathered while the other
-  // tile computes), double-buffered by step parity with one.
-  __shared__ f16x8 hbuf[2][KCH * FV];
+  // h of tile i in fragment order, double-buffered by step: step t reads h_{t-1} from hbuf[i][t & 1]
+  // and gathers h_t into hbuf[i][(t + 1) & 1].
+  __shared__ f16x8 hbuf[NTI][2][KCH * FV];
   __shared__ f16x8 ring[NTI][2][KCH * FV];  // layer input x_t of tile i in slot t & 1
   __shared__ float s_bias[4][HS];
   __shared__ int s_fail;
@@ -157,7 +158,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     }
   };
 #pragma unroll
-  for (int i = 0; i < NTI; ++i) fill_h0(i, hbuf[i]);
+  for (int i = 0; i < NTI; ++i) fill_h0(i, hbuf[i][0]);
   for (int idx = threadIdx.x; idx < NTI * 2 * KCH * FV; idx += NT)
     ring[idx / (2 * KCH * FV)][(idx / (KCH * FV)) & 1][idx % (KCH * FV)] = f16x8{};
   __syncthreads();  // s_bias, hbuf and the ring complete
@@ -170,9 +171,8 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     for (int j = 0; j < NJ; ++j) bias[q][j] = s_bias[q][wave * UPW + kgx + 4 * j];
 
   // ---- layer input: staged into the LDS ring in 1 KB pieces, D steps ahead ----
-  // Every phase issues the same memory operations on every path (the hand-off stores, BPW piece
-  // loads and one counter load; lanes and layers without a use for one address it out of range or
-  // at a dummy word), so the compiler can count exactly what a poll's wait covers.
+  // The pieces are loaded unconditionally (lanes past the input address it out of range), so that
+  // every path of a step issues the same loads.
   const int per = has_up ? KCH * FV : a.g_in0 * 16;  // f16x8 per step in the source
   const size_t hstep = (size_t)KCH * FV;
   // Descriptor of tile i's input of step s (word 3 0x00020000: DATA_FORMAT = 32 bit, which untyped
@@ -206,14 +206,14 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   // ---- hand-off publication and its check by the next layer ----
   // A (layer, tile) counter counts groups of G steps times the S slices: thread 0 of each slice
   // adds a group once its workgroup's hand-off stores of that group are complete.  Wave 0 reads the
-  // upstream counter every phase of a tile (used a phase of that tile later) and shares it in LDS.
+  // upstream counter every step (used a step later) and shares it in LDS.
   constexpr int CS = kSlicedCounterStride;
   auto up_ctr = [&](int i) -> uint32_t* { return a.counters + ((size_t)(layer - 1) * a.ntile + tile0 + i) * CS; };
   auto my_ctr = [&](int i) -> uint32_t* { return a.counters + ((size_t)layer * a.ntile + tile0 + i) * CS; };
   __shared__ uint32_t s_up[NTI];  // upstream counter of tile i as last read by wave 0
   int pub[NTI];                   // groups of tile i published (thread 0)
   int avail[NTI];                 // groups of tile i known published upstream (this wave)
-  uint32_t cup[NTI];              // wave 0: upstream counter of tile i, loaded a phase of the tile earlier
+  uint32_t cup[NTI];              // wave 0: upstream counter of tile i, loaded a step earlier
 #pragma unroll
   for (int i = 0; i < NTI; ++i) {
     pub[i] = 0;
@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   auto load_counter = [&](int i) {
     if (has_up && wave == 0) cup[i] = __hip_atomic_load(up_ctr(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  // Thread 0, after a phase's barrier: the hand-off stores of tile i's steps < n are complete (each
+  // Thread 0, after a step's barrier: the hand-off stores of tile i's steps < n are complete (each
   // was issued before a poll its wave has waited for).
   auto publish = [&](int i, int n) {
     const int groups = n >= Tt ? (Tt + G - 1) / G : n / G;
@@ -331,16 +331,14 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   int gdst[2 * NLD];
 #pragma unroll
   for (int r = 0; r < 2 * NLD; ++r) gdst[r] = word_dst(2 * ((int)threadIdx.x + (r >> 1) * NT) + (r & 1));
-  // Poll results: one set for both tiles (a tile's polls are issued at the end of its phase and
-  // gathered in the next phase, before the other tile's polls are issued).
-  uint64_t wv[2 * NLD];
+  uint64_t wv[NTI][2 * NLD];  // poll results of each tile
   // Poll p of tile i, step t: words 2 (tid + p NT) and + 1 of the slot, one 16-byte load with sc1
   // (each word is written by one aligned 8-byte store and lies inside the load, so it is read whole;
   // its own tag validates it).
   auto poll = [&](int i, int t, int p) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(slot_rs(i, t), threadIdx.x * 16u, p * NT * 16, 16);
-    wv[2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
-    wv[2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
+    wv[i][2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+    wv[i][2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
   };
   // Tile i's h_t to the siblings: one word from each writer lane (the others address no word).
   auto send = [&](int i, int t) {
@@ -366,10 +364,10 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     else
       __builtin_amdgcn_raw_buffer_store_b64(wd, slot_rs(i, t), woff, 0, 16);
   };
-  // The polls of tile i's step t, issued late in the phase (after the input part), when the
-  // siblings' words are usually written: a poll that finds a stale word costs a round trip at the
-  // gather.  Loads and stores retire in issue order, so the gather's wait covers nothing issued
-  // after these loads.
+  // The polls of tile i's step t, issued after the tile's word and (two tiles) the other tile's cell
+  // update, when the siblings' words are usually written: a poll that finds a stale word costs a
+  // round trip at the gather.  Loads and stores retire in issue order, so the gather's wait covers
+  // nothing issued after these loads.
   auto issue_poll = [&](int i, int t) {
 #pragma unroll
     for (int p = 0; p < NLD; ++p) poll(i, t, p);
@@ -382,7 +380,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < 2 * NLD; ++r) ready = ready && xw_tag(wv[r]) == want;
+      for (int r = 0; r < 2 * NLD; ++r) ready = ready && xw_tag(wv[i][r]) == want;
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -400,18 +398,18 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
       for (int p = 0; p < NLD; ++p)
-        if (xw_tag(wv[2 * p]) != want || xw_tag(wv[2 * p + 1]) != want) poll(i, t, p);
+        if (xw_tag(wv[i][2 * p]) != want || xw_tag(wv[i][2 * p + 1]) != want) poll(i, t, p);
     }
     uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
 #pragma unroll
     for (int r = 0; r < 2 * NLD; ++r) {
-      d32[gdst[r]] = xw_dec_pair((uint32_t)wv[r]);
-      d32[gdst[r] + D2] = xw_dec_pair((uint32_t)(wv[r] >> 32));
+      d32[gdst[r]] = xw_dec_pair((uint32_t)wv[i][r]);
+      d32[gdst[r] + D2] = xw_dec_pair((uint32_t)(wv[i][r] >> 32));
     }
   };
-  // The loads of this wave's previous phase of tile i (input piece, counter) were issued before the poll it
-  // has just waited for, so they are complete: the empty asm tells the compiler, which would
-  // otherwise wait for them as loads in flight where they are read.
+  // The loads of this wave's previous step for tile i (input piece, counter) were issued before
+  // the polls it has just waited for, so they are complete: the empty asm tells the compiler, which
+  // would otherwise wait for them as loads in flight where they are read.
   auto settle = [&](int i) {
 #pragma unroll
     for (int b = 0; b < BPW; ++b) asm volatile("" : "+v"(pc[i][b]));
@@ -420,7 +418,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
 
   // Hand-off to the next layer: h_s of tile i, this slice's HS units, from its fragment-ordered h
   // block to the hand-off buffer (the same order), one 16-byte sc1 store per thread of waves 0 ..
-  // HS / 32 - 1, a phase after the gather that completed it.
+  // HS / 32 - 1, a step after the gather that completed it.
   constexpr int CPY = HS / 32 * FV;  // f16x8 of a slice's units per step
   auto copy_out = [&](int i, int s_, const f16x8* src) {
     if (!has_down || (int)threadIdx.x >= CPY) return;
@@ -488,98 +486,60 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   lds_barrier();  // step 0 overwrites ring slot 0 (with x_2) once every wave has read x_0
 
   // ---- steps ----
-  // Phase (i, t) of a two-tile workgroup: h_{t-1} W_hh^T and the cell update of tile i; the other
-  // tile's gather (tile 1's of step t - 1 for tile 0, tile 0's of step t for tile 1); tile i's
-  // input of step t + 2 into the ring; tile i's word and hand-off stores; the input piece of step
-  // t + 3 and the counter; x_{t+1} W_ih^T; the polls of step t; one barrier, after which thread 0
-  // publishes.  One tile: the tile's own polls, hand-off and gather follow its input part,
-  // into the other h buffer.  Probes are written once both tiles have completed a step.
-  // The phases after the cell update and gather: ring input, word, input part, polls, hand-off,
-  // next input piece and counter, barrier, publication.  False if a wait of the workgroup failed.
-  auto finish_phase = [&](int i, int t) -> bool {
-    if constexpr (NTI == 2) {
-      // The polls go last: the next phase's gather waits for them alone, and the input piece and
-      // counter (issued before the input part) have the time of the input part and of the polls'
-      // round trip to arrive.
+  // Step t, for both tiles of a two-tile workgroup at once (the exchange's round trip, the memory
+  // issue and the barrier are paid once per step, not per tile): h_{t-1} W_hh^T; each tile's cell
+  // update, output sequence and word; the polls of step t, each followed by one tile's input part
+  // x_{t+1} W_ih^T, which covers the round trip (a poll issued right after the tile's own word would
+  // often find the siblings' words not yet written); the gathers into the other h buffer; then,
+  // off the step's chain, the input of step t + 2 into the ring, the hand-off copy of h_{t-1}, the
+  // input pieces of step t + 3 and the counter (issued after the gathers, so that no wait of this
+  // step covers them); one barrier, after which thread 0 publishes.
+  for (int t = 0; ok && t < Tt; ++t) {
+#pragma unroll
+    for (int i = 0; i < NTI; ++i) rec_mfma(i, hbuf[i][t & 1]);
+#pragma unroll
+    for (int i = 0; i < NTI; ++i) {
+      cell(i, t);
+      store_out_seq(i, t);
+      send(i, t);
+    }
+#pragma unroll
+    for (int i = 0; i < NTI; ++i) {
+      if constexpr (NTI == 2) issue_poll(i, t);
+      if (t + 1 < Tt) input_mfma(i, t + 1);
+      if constexpr (NTI == 1) issue_poll(i, t);
+    }
+#pragma unroll
+    for (int i = 0; i < NTI; ++i) gather(i, t, hbuf[i][(t + 1) & 1]);
+#pragma unroll
+    for (int i = 0; i < NTI; ++i) {
       settle(i);
       store_piece(i, t + 2);
-      send(i, t);
-      if (t > 0) copy_out(i, t - 1, hbuf[i]);
+      if (t > 0) copy_out(i, t - 1, hbuf[i][t & 1]);
       if (threadIdx.x == 0) s_up[i] = cup[i];
       if (has_up && !need_input(i, clamp_step(t + D))) s_fail = 1;
       load_piece(i, clamp_step(t + D));
       load_counter(i);
-      if (t + 1 < Tt) input_mfma(i, t + 1);
-      issue_poll(i, t);
-    } else {
-      // One tile gathers its own polls within the phase: the input piece and counter are issued
-      // after the gather, so that its wait does not include them.
-      send(0, t);
-      if (t + 1 < Tt) input_mfma(0, t + 1);
-      issue_poll(0, t);
-      gather(0, t, hbuf[(t + 1) & 1]);
-      settle(0);
-      store_piece(0, t + 2);
-      if (t > 0) copy_out(0, t - 1, hbuf[t & 1]);
-      if (threadIdx.x == 0) s_up[0] = cup[0];
-      if (has_up && !need_input(0, clamp_step(t + D))) s_fail = 1;
-      load_piece(0, clamp_step(t + D));
-      load_counter(0);
     }
     lds_barrier();
-    if (has_down) publish(i, t - 1);
-    return __builtin_amdgcn_readfirstlane(s_fail) == 0;
-  };
-  auto after_step = [&](int t) {
+    if (has_down) {
+#pragma unroll
+      for (int i = 0; i < NTI; ++i) publish(i, t - 1);
+    }
+    if (__builtin_amdgcn_readfirstlane(s_fail) != 0) {
+      ok = false;
+      break;
+    }
     if (t + 1 == probe_next) {
       write_probe(probe_i);
       ++probe_i;
       probe_next = probe_i < a.n_probe ? __builtin_amdgcn_readfirstlane(a.probe_steps[probe_i]) : -1;
     }
-  };
-  if constexpr (NTI == 2) {
-    // Phase (0, 0) has no gather to complete; the loop runs phase (1, t), then (0, t + 1), each
-    // after the other tile's gather (so every phase in the loop has one).
-    if (ok && Tt > 0) {
-      rec_mfma(0, hbuf[0]);
-      cell(0, 0);
-      store_out_seq(0, 0);
-      ok = finish_phase(0, 0);
-    }
-    for (int t = 0; ok && t < Tt; ++t) {
-      rec_mfma(1, hbuf[1]);
-      cell(1, t);
-      store_out_seq(1, t);
-      gather(0, t, hbuf[0]);
-      if (!(ok = finish_phase(1, t))) break;
-      after_step(t);
-      if (t + 1 == Tt) break;
-      rec_mfma(0, hbuf[0]);
-      cell(0, t + 1);
-      store_out_seq(0, t + 1);
-      gather(1, t, hbuf[1]);
-      ok = finish_phase(0, t + 1);
-    }
-  } else {
-    for (int t = 0; ok && t < Tt; ++t) {
-      rec_mfma(0, hbuf[t & 1]);
-      cell(0, t);
-      store_out_seq(0, t);
-      if (!(ok = finish_phase(0, t))) break;
-      after_step(t);
-    }
   }
-  // The last gather of a two-tile workgroup (tile 1's last step) and the final publication, once
-  // every wave's hand-off stores are complete.
+  // The last step's hand-off copy and the final publication, once every wave's copies are complete.
   if (ok && Tt > 0) {
-    if constexpr (NTI == 2) {
-      gather(1, Tt - 1, hbuf[1]);
-      __syncthreads();
-      copy_out(0, Tt - 1, hbuf[0]);
-      copy_out(1, Tt - 1, hbuf[1]);
-    } else {
-      copy_out(0, Tt - 1, hbuf[Tt & 1]);
-    }
+#pragma unroll
+    for (int i = 0; i < NTI; ++i) copy_out(i, Tt - 1, hbuf[i][Tt & 1]);
     wait_vmem_all();
     __syncthreads();
     ok = __builtin_amdgcn_readfirstlane(s_fail) == 0;
@@ -588,7 +548,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       for (int i = 0; i < NTI; ++i) publish(i, Tt);
     }
   }
-  auto hfinal = [&](int i) -> f16x8* { return NTI == 2 ? hbuf[i] : hbuf[Tt & 1]; };
+  auto hfinal = [&](int i) -> f16x8* { return hbuf[i][Tt & 1]; };
   // Rows of length 0 keep their h0, which the packed exchange may not carry intact: restore their
   // h in the final buffer before the head reads it.
   if (ok && a.lengths && Tt > 0) {

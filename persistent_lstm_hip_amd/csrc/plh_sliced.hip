@@ -240,7 +240,9 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     const int g = s / G;
     if (g < avail[i]) return true;
     const uint32_t need = (uint32_t)S * (uint32_t)(g + 1);
-    uint32_t v = __builtin_amdgcn_readfirstlane(*(volatile uint32_t*)&s_up[i]);
+    // An LDS read (each step's barrier orders it after wave 0's write); through a generic pointer it
+    // would be a flat load, whose wait covers every global access in flight.
+    uint32_t v = __builtin_amdgcn_readfirstlane(s_up[i]);
     if (v < need) {
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
       for (;;) {
@@ -328,15 +330,24 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     const int u0 = sl * HS + wv_ * UPW + (rem / 16) * KW;
     return ((u0 >> 3) * 16 + (rem & 15)) * 4 + ((u0 & 7) >> 1);
   };
+  // Poll p of a thread reads words m and m + 1 of every slice's block: waves 0-3 the words that the
+  // slices' waves 0-3 write (the first half of a block), waves 4-7 the other half.  The second wave
+  // of each SIMD finishes its MFMAs later (the matrix core serves the older wave first), and so do
+  // its words; polled by the waves that are late themselves, they are usually written when polled.
+  auto poll_word = [](int tid, int p) -> int {
+    const int half = tid / (NT / 2), j = tid % (NT / 2) + p * (NT / 2);
+    return (j / (SB / 4)) * SB + half * (SB / 2) + 2 * (j % (SB / 4));
+  };
   int gdst[2 * NLD];
 #pragma unroll
-  for (int r = 0; r < 2 * NLD; ++r) gdst[r] = word_dst(2 * ((int)threadIdx.x + (r >> 1) * NT) + (r & 1));
+  for (int r = 0; r < 2 * NLD; ++r) gdst[r] = word_dst(poll_word((int)threadIdx.x, r >> 1) + (r & 1));
   uint64_t wv[NTI][2 * NLD];  // poll results of each tile
-  // Poll p of tile i, step t: words 2 (tid + p NT) and + 1 of the slot, one 16-byte load with sc1
+  // Poll p of tile i, step t: words poll_word(tid, p) and + 1 of the slot, one 16-byte load with sc1
   // (each word is written by one aligned 8-byte store and lies inside the load, so it is read whole;
-  // its own tag validates it).
+  // its own tag validates it).  The offset is a per-wave part (slice and half) plus 16 bytes per lane.
+  const uint32_t poll_off = (uint32_t)poll_word((int)threadIdx.x, 0) * 8u;
   auto poll = [&](int i, int t, int p) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(slot_rs(i, t), threadIdx.x * 16u, p * NT * 16, 16);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(slot_rs(i, t), poll_off, p * (NT / 2) / (SB / 4) * SB * 8, 16);
     wv[i][2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
     wv[i][2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
   };

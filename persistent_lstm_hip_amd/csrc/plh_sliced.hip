@@ -177,10 +177,18 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   const size_t hstep = (size_t)KCH * FV;
   // Descriptor of tile i's input of step s (word 3 0x00020000: DATA_FORMAT = 32 bit, which untyped
   // buffer accesses need on CDNA).
+  // Step-0 addresses of each tile's input and hand-off sequences (a step is `per`, resp. hstep,
+  // f16x8 further), computed once.
+  const f16x8* in_base[NTI];
+  f16x8* out_base[NTI];
+#pragma unroll
+  for (int i = 0; i < NTI; ++i) {
+    in_base[i] = has_up ? a.hseq + ((size_t)(layer - 1) * a.ntile + tile0 + i) * a.T * hstep
+                        : a.xp + (size_t)(tile0 + i) * a.T * per;
+    out_base[i] = a.hseq + ((size_t)layer * a.ntile + tile0 + i) * a.T * hstep;
+  }
   auto in_rs = [&](int i, int s) {
-    const f16x8* src = has_up ? a.hseq + (((size_t)(layer - 1) * a.ntile + tile0 + i) * a.T + s) * hstep
-                              : a.xp + ((size_t)(tile0 + i) * a.T + s) * per;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<f16x8*>(src), 0, per * 16, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<f16x8*>(in_base[i] + s * per), 0, per * 16, 0x00020000);
   };
   // Input piece of tile i, step s: block wave * BPW + b of the step, one f16x8 per lane.  Entries
   // past `per` (layer 0: x's K groups) read out of the descriptor's range, which returns zero.  The
@@ -316,7 +324,10 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   // wave * 16 NJ + (kgx / KW) * 16 + en of its slice's block, carrying units (eu, eu + 1) and
   // (eu + 4, eu + 5) (NJ = 2, from itself and lane + 16) or eu .. eu + 3 (NJ = 1, from lanes + 16,
   // + 32, + 48) of row en.
-  auto xr = [&](int i) -> uint64_t* { return a.xring + ((size_t)layer * a.ntile + tile0 + i) * 2 * C::kWords; };
+  uint64_t* xr_base[NTI];
+#pragma unroll
+  for (int i = 0; i < NTI; ++i) xr_base[i] = a.xring + ((size_t)layer * a.ntile + tile0 + i) * 2 * C::kWords;
+  auto xr = [&](int i) -> uint64_t* { return xr_base[i]; };
   const int pwoff = slice * SB + wave * 16 * NJ + (kgx / KW) * 16 + en;
   auto slot_rs = [&](int i, int t) {
     return __builtin_amdgcn_make_buffer_rsrc(xr(i) + (size_t)__builtin_amdgcn_readfirstlane(t & 1) * C::kWords, 0,
@@ -434,8 +445,8 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   auto copy_out = [&](int i, int s_, const f16x8* src) {
     if (!has_down || (int)threadIdx.x >= CPY) return;
     const int idx = slice * CPY + (int)threadIdx.x;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        a.hseq + (((size_t)layer * a.ntile + tile0 + i) * a.T + s_) * hstep, 0, (int)(hstep * 16), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(out_base[i] + s_ * (int)hstep, 0, (int)(hstep * 16), 0x00020000);
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, src[idx]),
                                            rs, (uint32_t)idx * 16u, 0, 16);
   };

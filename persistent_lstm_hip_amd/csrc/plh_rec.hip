@@ -385,13 +385,18 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       wv[2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
       wv[2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
     };
-    // The first wave of each SIMD (waves 0-3) finishes its cell updates ~500 cycles before the
-    // second (the matrix core serves the older wave first), so its first poll would find the words
-    // of the siblings' second waves not yet written and cost a round trip (~800 cycles under load).
-    // Waves 0-3 therefore wait 512 cycles before polling (the best of delays of 256-768 cycles in
-    // an instrumented copy; C4 -1.7% in interleaved runs, 11.79 -> 11.59 ms; a workgroup barrier
-    // here instead gained less).  Only the poll is delayed.
-    if (wave < 4) __builtin_amdgcn_s_sleep(8);
+    // A first poll that finds a sibling's word not yet written costs a round trip (~800 cycles
+    // under load), so every wave waits before polling: the first wave of each SIMD (waves 0-3)
+    // finishes its cell updates ~500 cycles before the second (the matrix core serves the older
+    // wave first) and waits 896 cycles, the second 384.  The branch is on a wave-uniform value:
+    // s_sleep ignores the exec mask, so under a lane-masked branch every wave would sleep.  In
+    // interleaved C4 runs on two boxes: no wait 12.23 ms, 512 cycles for all waves 11.92 / 11.48,
+    // 512 for waves 0-3 only 12.01, 896 / 384 11.27-11.85 (-1.8% to -2.4%); 768-1152 / 256-384 within
+    // 1% of it.  Only the poll is delayed.
+    if (__builtin_amdgcn_readfirstlane(wave) < 4)
+      __builtin_amdgcn_s_sleep(14);
+    else
+      __builtin_amdgcn_s_sleep(6);
 #pragma unroll
     for (int p = 0; p < NW / 2; ++p)
       if (p < nld) pload(p);

@@ -151,12 +151,22 @@ struct Rec {
 // (never an h) and come back as NaN.  The bit is cleared in every value sent, so the tag is always
 // intact.  Rows of length 0 keep their h0, which may use the bit: their exchanged values only feed
 // their own frozen rows, and the kernels restore h0 before it is read as a result.
-__device__ __forceinline__ uint32_t xw_enc_half(uint32_t b) {
-  return (b & 0x7C00u) == 0x7C00u ? (b & 0x8000u) | 0x3E00u : b & 0xBFFFu;
-}
-__device__ __forceinline__ uint32_t xw_enc_half(_Float16 h) { return xw_enc_half((uint32_t)__builtin_bit_cast(uint16_t, h)); }
-__device__ __forceinline__ uint32_t xw_enc_pair(uint32_t p) {
-  return xw_enc_half(p & 0xFFFFu) | (xw_enc_half(p >> 16) << 16);
+// The xw_* helpers are also host functions, so that a host program can check them exhaustively.
+typedef unsigned short xw_u16x2 __attribute__((ext_vector_type(2)));
+typedef short xw_s16x2 __attribute__((ext_vector_type(2)));
+// Two fp16 (bit patterns, low and high half) made exchange-safe: a half with an all-ones exponent
+// (NaN, infinity) becomes sign | 0x3E00 (+-1.5), every other half loses bit 14.  Per half, the
+// exponent bits plus 0x0400 carry into bit 15 exactly when they are all ones; an arithmetic shift
+// makes that a mask of the half, and one bit-field insert picks marker or value.  Packed 16-bit
+// operations for both halves (v_pk_add_u16, v_pk_ashrrev_i16, v_bfi_b32) instead of a compare and
+// select each.
+__host__ __device__ __forceinline__ uint32_t xw_enc_pair(uint32_t p) {
+  const xw_u16x2 f = __builtin_bit_cast(xw_u16x2, p & 0x7C007C00u) + xw_u16x2{0x0400, 0x0400};
+  uint32_t special = __builtin_bit_cast(uint32_t, __builtin_bit_cast(xw_s16x2, f) >> (short)15);
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("" : "+v"(special));  // keeps the mask a mask (else it is rebuilt as per-half compares and selects)
+#endif
+  return (special & ((p & 0x80008000u) | 0x3E003E00u)) | (~special & p & 0xBFFFBFFFu);
 }
 // Two fp16 of a word back, the tag bits cleared and +-1.5 restored as NaN.  Per 16-bit half, m (the
 // value without sign and tag bit) is <= 0x3C00 for every h (|h| <= 1) and 0x3E00 for the marker;
@@ -164,21 +174,20 @@ __device__ __forceinline__ uint32_t xw_enc_pair(uint32_t p) {
 // the marker into NaN (0x7E00) where the tag bit was.  One packed 16-bit add for both halves instead
 // of a compare and select each.  (Values 1.25 <= |x| < 2 other than the marker, which only the
 // frozen rows of length 0 can carry, also come back as NaN; those rows' h is restored from h0.)
-__device__ __forceinline__ uint32_t xw_dec_pair(uint32_t v) {
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  const u16x2 z = __builtin_bit_cast(u16x2, v & 0x3FFF3FFFu) + u16x2{0x4300, 0x4300};
+__host__ __device__ __forceinline__ uint32_t xw_dec_pair(uint32_t v) {
+  const xw_u16x2 z = __builtin_bit_cast(xw_u16x2, v & 0x3FFF3FFFu) + xw_u16x2{0x4300, 0x4300};
   return (v & 0xBFFFBFFFu) | ((__builtin_bit_cast(uint32_t, z) >> 1) & 0x40004000u);
 }
-__device__ __forceinline__ uint32_t xw_tag(uint64_t w) {
+__host__ __device__ __forceinline__ uint32_t xw_tag(uint64_t w) {
   return (uint32_t)(((w >> 14) & 1u) | ((w >> 29) & 2u) | ((w >> 44) & 4u) | ((w >> 59) & 8u));
 }
-__device__ __forceinline__ uint64_t xw_tag_bits(uint32_t tag) {
+__host__ __device__ __forceinline__ uint64_t xw_tag_bits(uint32_t tag) {
   return ((uint64_t)(tag & 1u) << 14) | ((uint64_t)((tag >> 1) & 1u) << 30) | ((uint64_t)((tag >> 2) & 1u) << 46) |
          ((uint64_t)((tag >> 3) & 1u) << 62);
 }
 // Tag of step t's words in a two-slot ring (slot t & 1): successive writes to a slot (steps t - 2
 // and t) differ, and none is 0 (the cleared ring).
-__device__ __forceinline__ uint32_t xw_step_tag(int t) { return (uint32_t)((t >> 1) % 15) + 1u; }
+__host__ __device__ __forceinline__ uint32_t xw_step_tag(int t) { return (uint32_t)((t >> 1) % 15) + 1u; }
 
 __device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -358,7 +358,8 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // partner lane + 16 (kgx + 1) eu + 1 and eu + 5.
     uint32_t pair_lo, pair_hi;
     {
-      const uint32_t mine = xw_enc_half(hcur[0]) | (xw_enc_half(hcur[1]) << 16);
+      const uint32_t mine = xw_enc_pair((uint32_t)__builtin_bit_cast(uint16_t, hcur[0]) |
+                                        ((uint32_t)__builtin_bit_cast(uint16_t, hcur[1]) << 16));
       const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
       pair_lo = __builtin_amdgcn_perm(other, mine, 0x05040100u);
       pair_hi = __builtin_amdgcn_perm(other, mine, 0x07060302u);

@@ -181,6 +181,11 @@ __host__ __device__ __forceinline__ uint32_t xw_dec_pair(uint32_t v) {
 __host__ __device__ __forceinline__ uint32_t xw_tag(uint64_t w) {
   return (uint32_t)(((w >> 14) & 1u) | ((w >> 29) & 2u) | ((w >> 44) & 4u) | ((w >> 59) & 8u));
 }
+// True if the tag bits of word w are want_bits (= xw_tag_bits of the wanted tag): one masked compare
+// of the 64-bit word instead of gathering its four tag bits.
+__host__ __device__ __forceinline__ bool xw_tag_is(uint64_t w, uint64_t want_bits) {
+  return ((w ^ want_bits) & 0x4000400040004000ull) == 0u;
+}
 __host__ __device__ __forceinline__ uint64_t xw_tag_bits(uint32_t tag) {
   return ((uint64_t)(tag & 1u) << 14) | ((uint64_t)((tag >> 1) & 1u) << 30) | ((uint64_t)((tag >> 2) & 1u) << 46) |
          ((uint64_t)((tag >> 3) & 1u) << 62);

@@ -278,7 +278,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     }
   };
 
-  uint64_t wv[NW];
+  uint64_t wv[NW] = {};  // poll results (words of waves with one load: the first two)
   // The next layer's input: h_t of this slice's 64 units x 16 rows, written a step later from
   // hbuf in 16-byte pieces, fragment-blocked: two contiguous 1 KB blocks (row block t * ntile + tile,
   // column blocks 2 slice and 2 slice + 1), one per wave.
@@ -351,6 +351,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // order, so the poll waits for nothing issued after it.
     // Tags of successive writes to a slot (steps t - 2, t) differ, and none is 0 (the cleared ring).
     const uint32_t want = xw_step_tag(t);
+    const uint64_t want_bits = xw_tag_bits(want);  // its bits as the words carry them
     // This step's ring slot, uniform by construction: the compiler would otherwise keep its address
     // in VGPRs (it flows through the lane-conditional store) and put every poll in a waterfall loop.
     uint64_t* const slot = ring + (size_t)__builtin_amdgcn_readfirstlane(t & 1) * PW;
@@ -363,7 +364,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
       pair_lo = __builtin_amdgcn_perm(other, mine, 0x05040100u);
       pair_hi = __builtin_amdgcn_perm(other, mine, 0x07060302u);
-      const uint64_t word = ((uint64_t)pair_lo | ((uint64_t)pair_hi << 32)) | xw_tag_bits(want);
+      const uint64_t word = ((uint64_t)pair_lo | ((uint64_t)pair_hi << 32)) | want_bits;
       if ((kgx & 1) == 0) {
         if (l2)
           __hip_atomic_store(slot + pwoff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -427,7 +428,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < NW; ++r) ready = ready && ((r >> 1) >= nld || xw_tag(wv[r]) == want);
+      for (int r = 0; r < NW; ++r) ready = ready & ((r >> 1) >= nld || xw_tag_is(wv[r], want_bits));
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -445,7 +446,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
       for (int p = 0; p < NW / 2; ++p)
-        if (p < nld && (xw_tag(wv[2 * p]) != want || xw_tag(wv[2 * p + 1]) != want)) pload(p);
+        if (p < nld && !(xw_tag_is(wv[2 * p], want_bits) & xw_tag_is(wv[2 * p + 1], want_bits))) pload(p);
     }
     // gn's load was issued before this step's poll, so it has completed (loads retire in order);
     // the empty asm tells the compiler, which would otherwise count the copy below as a read of a

@@ -397,12 +397,13 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   // Complete the gather of tile i, step t, into dst: re-poll the words whose tag is not step t's
   // yet (bounded wait; a failure sets s_fail), then scatter them into fragment order.
   auto gather = [&](int i, int t, f16x8* dst) {
-    const uint32_t want = xw_step_tag(t);
+    const uint64_t want = xw_tag_bits(xw_step_tag(t));
     uint64_t t0 = 0;
     for (int spin = 0;; ++spin) {
+      // & rather than &&: every word is tested (no lane-masked branch per word)
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < 2 * NLD; ++r) ready = ready && xw_tag(wv[i][r]) == want;
+      for (int r = 0; r < 2 * NLD; ++r) ready = ready & xw_tag_is(wv[i][r], want);
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -420,7 +421,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
       for (int p = 0; p < NLD; ++p)
-        if (xw_tag(wv[i][2 * p]) != want || xw_tag(wv[i][2 * p + 1]) != want) poll(i, t, p);
+        if (!(xw_tag_is(wv[i][2 * p], want) & xw_tag_is(wv[i][2 * p + 1], want))) poll(i, t, p);
     }
     uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
 #pragma unroll

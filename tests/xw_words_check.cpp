@@ -1,5 +1,5 @@
 // Host check of the packed exchange-word helpers of plh_device.h (xw_enc_pair, xw_dec_pair,
-// xw_tag, xw_tag_bits, xw_step_tag), built and run by tests/test_xw_words.py.  The helpers use
+// xw_tag, xw_tag_is, xw_tag_bits, xw_step_tag), built and run by tests/test_xw_words.py.  The helpers use
 // packed 16-bit arithmetic; here they are compared, exhaustively over one 16-bit half and a stride
 // over the other, with their per-half definitions:
 //   encode: a half with an all-ones exponent (NaN, infinity) -> sign | 0x3E00, any other -> bit 14 cleared
@@ -64,6 +64,14 @@ int main() {
       if (bad++ < 5) std::printf("tag %u\n", tag);
     }
   }
+  // xw_tag_is: the masked compare agrees with the extracted tag for every tag and word pattern
+  for (uint32_t tag = 0; tag < 16; ++tag)
+    for (uint32_t k = 0; k < 65536; ++k) {
+      const uint64_t w = ((uint64_t)(k * 2654435761u) << 32 | (k * 40503u)) ^ ((uint64_t)k << 14);
+      if (xw_tag_is(w, xw_tag_bits(tag)) != (xw_tag(w) == tag)) {
+        if (bad++ < 5) std::printf("tag_is %u 0x%016llx\n", tag, (unsigned long long)w);
+      }
+    }
   for (int t = 0; t < 100000; ++t) {
     const uint32_t a = xw_step_tag(t), b = xw_step_tag(t + 2);
     if (a < 1u || a > 15u || a == b) {

@@ -300,7 +300,13 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     f16x8* const hnext = hbuf[(t + 1) & 1];
     // The gate sums of the wave's two tiles over all of K (X0: plus x_t W_ih^T), two independent
     // MFMA chains fed by one 16-byte LDS read per K chunk.
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    // The accumulators start at bias + x_t W_ih^T (X0: at the bias), added here, where the second
+    // wave of a SIMD waits for the matrix core anyway, rather than between the MFMAs and the gate math.
+    f32x4 acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[j][q] = X0 ? bias[q][j] : bias[q][j] + (float)gp[2 * q + j];
     if constexpr (X0) {
       acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[0], gp, acc[0], 0, 0, 0);
       acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[1], gp, acc[1], 0, 0, 0);
@@ -331,7 +337,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          z[q][j] = X0 ? acc[j][q] + bias[q][j] : acc[j][q] + bias[q][j] + (float)gp[2 * q + j];
+          z[q][j] = acc[j][q];
       float cn[2] = {c[0], c[1]}, hn[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn[j], hn[j]);

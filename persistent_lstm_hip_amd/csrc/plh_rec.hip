@@ -233,10 +233,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
 
   // Packed exchange (xw_* words): a word carries units eu, eu + 1 (low half) and eu + 4, eu + 5 (high
   // half) of one row from a lane with even kgx, which holds eu and eu + 4 and takes eu + 1 and eu + 5
-  // from its partner lane + 16.  Half the bytes of one word per pair with a 32-bit tag.  Words are in
-  // writer order [slice][wave][32].
+  // from its partner lane + 16.  Words are in writer order [slice][wave][row en][kgx / 2]: the two
+  // words of a 16-byte load are units 8 w .. 8 w + 7 of one row, one f16x8 of h's fragment order.
   uint64_t* ring = a.xring + (size_t)tile * 2 * C::kWords;  // a slot of PW words per step parity
-  const int pwoff = (slice * 8 + wave) * 32 + (kgx >> 1) * 16 + en;  // this lane's word (even kgx)
+  const int pwoff = (slice * 8 + wave) * 32 + en * 2 + (kgx >> 1);  // this lane's word (even kgx)
   // A workgroup gathers the 7 sibling slices' words (its own pairs go to hbuf from registers): load
   // k of a thread reads words 2 (tid % 128) and 2 (tid % 128) + 1 of sibling block 4 k + tid / 128
   // (the blocks in slice order without this workgroup's own), so waves 0-5 issue 2 loads, 6-7 one.
@@ -246,14 +246,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     const int r = 4 * k + quarter;
     return r + (r >= slice ? 1 : 0);
   };
-  // LDS destination (u32 index into hbuf) of the first pair of the r-th word this thread gathers;
-  // the second pair (4 units on) is 2 further.
-  auto gdst = [&](int r) -> int {
-    const int wq = 2 * (threadIdx.x & 127) + (r & 1);  // word within the sibling's block
-    const int wv_ = wq >> 5, en_ = wq & 15, kgx_ = 2 * ((wq >> 4) & 1);
-    const int eu_ = sib(r >> 1) * HS + wv_ * 8 + kgx_;
-    return ((eu_ >> 3) * 16 + en_) * 4 + ((eu_ & 7) >> 1);
-  };
+  // hbuf position (f16x8 index) of load k of this thread: units 8 (tid % 128 / 16) .. + 7 of the
+  // sibling's block, row tid % 16, i.e. (sib * HS / 8 + tid % 128 / 16) * 16 + tid % 16; a wave's
+  // loads fill 64 consecutive f16x8 (1 KB), so its one 16-byte LDS store per load is conflict-free.
+  auto gdst16 = [&](int k) -> int { return sib(k) * (HS / 8) * 16 + (int)(threadIdx.x & 127); };
   const int own_dst = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's word's first pair in hbuf (even kgx)
   // b_ih + b_hh of this lane's units (eu + 4 j) by gate, in registers for the whole sequence.
   float bias[4][2];
@@ -466,13 +462,14 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     }
     asm volatile("" : "+v"(gn));
     gp = gn;
-    uint32_t* hb32 = reinterpret_cast<uint32_t*>(hnext);
 #pragma unroll
-    for (int r = 0; r < NW; ++r)
-      if ((r >> 1) < nld) {
-        const int d = gdst(r);
-        hb32[d] = xw_dec_pair((uint32_t)wv[r]);
-        hb32[d + 2] = xw_dec_pair((uint32_t)(wv[r] >> 32));
+    for (int k = 0; k < NW / 2; ++k)
+      if (k < nld) {
+        // words 2 k (units +0, +1 | +4, +5) and 2 k + 1 (+2, +3 | +6, +7) of one row
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = {xw_dec_pair((uint32_t)wv[2 * k]), xw_dec_pair((uint32_t)wv[2 * k + 1]),
+                         xw_dec_pair((uint32_t)(wv[2 * k] >> 32)), xw_dec_pair((uint32_t)(wv[2 * k + 1] >> 32))};
+        hnext[gdst16(k)] = __builtin_bit_cast(f16x8, v);
       }
     lds_barrier();
     return __builtin_amdgcn_readfirstlane(s_fail) == 0;

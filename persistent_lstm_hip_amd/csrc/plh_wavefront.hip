@@ -169,9 +169,17 @@ __device__ __forceinline__ void wavefront_body(const ForwardArgs& a, WavefrontLd
   // zero from the initialisation).  Every lane loads (indices clamped into the chunk), so the loads
   // write R directly.
   f16x8 R[RN];
+  // A full chunk of a full-width source (layers >= 1) needs no clamping or lane conditions (8-row
+  // tiles; the 16-row kernel has no VGPRs for a second copy of these paths).
+  const bool full_width = ROWS == 8 && per == KCI * FV;
   auto load_chunk = [&](int k) {
     const int ns_k = min(CH, Tt - k * CH);
     const f16x8* src = in_seq + (size_t)k * CH * per;
+    if (full_width && ns_k == CH) {
+#pragma unroll
+      for (int i = 0; i < RN; ++i) R[i] = src[(int)threadIdx.x + i * NT];
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < RN; ++i) {
       const int p = (int)threadIdx.x + i * NT;
@@ -182,6 +190,11 @@ __device__ __forceinline__ void wavefront_body(const ForwardArgs& a, WavefrontLd
   auto store_chunk = [&](int k) {
     const int ns_k = min(CH, Tt - k * CH);
     f16x8* rb = ring + (k & 1) * kRingBuf;
+    if (full_width && ns_k == CH) {
+#pragma unroll
+      for (int i = 0; i < RN; ++i) rb[(int)threadIdx.x + i * NT] = R[i];
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < RN; ++i) {
       const int p = (int)threadIdx.x + i * NT;
@@ -197,6 +210,14 @@ __device__ __forceinline__ void wavefront_body(const ForwardArgs& a, WavefrontLd
     const uint64_t* hb = reinterpret_cast<const uint64_t*>(hist + (k & 1) * kHistBuf);
     uint64_t* dst = reinterpret_cast<uint64_t*>(out_seq_h + (size_t)k * CH * hstep);
     uint64_t v[2 * RN];
+    if (ROWS == 8 && nw == 2 * RN * NT) {  // a full chunk: every thread copies 2 RN words
+#pragma unroll
+      for (int i = 0; i < 2 * RN; ++i) v[i] = hb[(int)threadIdx.x + i * NT];
+#pragma unroll
+      for (int i = 0; i < 2 * RN; ++i)
+        __hip_atomic_store(dst + threadIdx.x + i * NT, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 2 * RN; ++i) v[i] = hb[min((int)threadIdx.x + i * NT, nw - 1)];
 #pragma unroll

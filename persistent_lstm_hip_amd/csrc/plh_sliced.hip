@@ -50,7 +50,8 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   constexpr int PW = S * SB;              // packed words of one step of a tile (4 HP)
   constexpr int NLD = PW / 2 / NT;        // 16-byte poll loads per thread and step
   constexpr int D2 = NJ == 2 ? 2 : 1;     // u32 distance in hbuf between a word's two pairs
-  constexpr int BPW = KCH / 8;            // 1 KB input blocks each wave stages per step
+  constexpr int SW = HP == 256 ? 4 : 8;   // waves that stage the input pieces
+  constexpr int BPW = KCH / SW;           // 1 KB input blocks each of them stages per step
   constexpr int G = 2;                    // steps per publication of the hand-off
   constexpr int D = 3;                    // steps between an input's load and its use
   constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every range: stores dropped
@@ -190,12 +191,19 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   auto in_rs = [&](int i, int s) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<f16x8*>(in_base[i] + s * per), 0, per * 16, 0x00020000);
   };
+  // Waves 0 .. SW - 1 stage the input.  At padded H 256 these are the first waves of the SIMDs,
+  // which finish a step's work earlier (the matrix core serves them first) and would otherwise wait
+  // at the step's barrier, while the second waves' part of the step is its critical path (C3 -1.1%,
+  // B = 64 -6.7%); at H 512 a step's input is twice as large and all waves stage it (with four, B = 64
+  // was 3.2% slower).
+  const bool stager = SW == 8 || __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < SW;
   // Input piece of tile i, step s: block wave * BPW + b of the step, one f16x8 per lane.  Entries
   // past `per` (layer 0: x's K groups) read out of the descriptor's range, which returns zero.  The
   // previous layer's h is read with sc1: it was written with sc1 by other CUs, and its counter was
   // seen before the load is issued.
   f16x8 pc[NTI][BPW];
   auto load_piece = [&](int i, int s) {
+    if (!stager) return;
     const __amdgpu_buffer_rsrc_t rs = in_rs(i, s);
 #pragma unroll
     for (int b = 0; b < BPW; ++b) {
@@ -207,6 +215,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     }
   };
   auto store_piece = [&](int i, int s) {
+    if (!stager) return;
 #pragma unroll
     for (int b = 0; b < BPW; ++b) ring[i][s & 1][(wave * BPW + b) * FV + lane] = pc[i][b];
   };
@@ -486,7 +495,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   if (ok && Tt > 0) {
 #pragma unroll
     for (int i = 0; i < NTI; ++i) {
-      if (has_up && !need_input(i, clamp_step(D - 1))) ok = false;
+      if (has_up && stager && !need_input(i, clamp_step(D - 1))) ok = false;
       if (!ok) break;
 #pragma unroll
       for (int s = 0; s < D - 1; ++s) {
@@ -540,7 +549,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
       store_piece(i, t + 2);
       if (t > 0) copy_out(i, t - 1, hbuf[i][t & 1]);
       if (threadIdx.x == 0) s_up[i] = cup[i];
-      if (has_up && !need_input(i, clamp_step(t + D))) s_fail = 1;
+      if (has_up && stager && !need_input(i, clamp_step(t + D))) s_fail = 1;
       load_piece(i, clamp_step(t + D));
       load_counter(i);
     }

@@ -354,7 +354,18 @@ __device__ __forceinline__ void wavefront_body(const ForwardArgs& a, WavefrontLd
         hcur[j] = (_Float16)hn;
       }
     };
-    if constexpr (ROWS == 8) {
+    if constexpr (ROWS == 8 && RAGGED) {
+      // With ragged rows (the selects on `live` add VALU work) the gate math goes first and the
+      // next step's input MFMAs follow it: 1.7-2.3% faster than the interleave below, which is
+      // the faster one without them.
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < UPL; ++j) cell_pair(j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < KIN * 4; ++m) input_mfma(m);
+      __builtin_amdgcn_sched_barrier(0);
+    } else if constexpr (ROWS == 8) {
       // Two pairs per lane (~80 VALU instructions per wave): one MFMA, then three VALU
       // instructions, and so on, so both waves of a SIMD keep the matrix core fed and neither
       // queues its gate math behind a burst of MFMAs.

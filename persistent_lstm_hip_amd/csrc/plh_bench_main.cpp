@@ -9,11 +9,14 @@
 //   plh_bench [--input 5] [--hidden 128] [--layers 4] [--output 24] [--batch 512] [--seq 1000]
 //             [--warmup 10] [--iters 100] [--ragged MIN] [--copy-mb N]
 //   plh_bench --gemm K [--cols N] [--batch 512] [--seq 1000] [--blocked 1] [--warmup 10] [--iters 100]
+//   plh_bench --issue
 //
 // --copy-mb N ends the run with three device-to-device copies of N MiB: a plain copy kernel of
 // known size, whose memory counters calibrate the forward's HBM traffic in a profiler.
 // --gemm K times plh_input_projection alone: [batch * seq, K] x [K, N] (N = --cols, default 4 K),
 // fragment-blocked by default (the layer-sequential path's layout), random fp16 operands.
+// --issue prints the SIMD issue rates of plh_probe_issue_rates (MFMA, v_exp_f32, v_fma_f32, alone,
+// beside each other in the two waves of a SIMD, and interleaved in one wave).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -135,9 +138,30 @@ int gemm_main(int argc, char** argv) {
   return 0;
 }
 
+// --issue: the issue-rate table of plh_probe_issue_rates, one JSON line per case.
+int issue_main() {
+  static const char* kNames[PLH_ISSUE_CASES] = {"mfma",     "exp",      "fma",      "mfma|mfma", "exp|exp",
+                                                "fma|fma",  "mfma|exp", "mfma|fma", "mfma+fma",  "mfma+exp"};
+  double c[2 * PLH_ISSUE_CASES];
+  if (plh_probe_issue_rates(c, 2 * PLH_ISSUE_CASES) != PLH_OK) {
+    std::fprintf(stderr, "plh_probe_issue_rates: %s\n", plh_last_error());
+    return 1;
+  }
+  for (int i = 0; i < PLH_ISSUE_CASES; ++i) {
+    if (std::strchr(kNames[i], '|'))
+      std::printf("{\"case\": \"%s\", \"cycles_per_inst_waves_0_3\": %.2f, \"cycles_per_inst_waves_4_7\": %.2f}\n",
+                  kNames[i], c[2 * i], c[2 * i + 1]);
+    else
+      std::printf("{\"case\": \"%s\", \"cycles_per_inst_waves_0_3\": %.2f}\n", kNames[i], c[2 * i]);
+  }
+  return 0;
+}
+
 int main(int argc, char** argv) {
-  for (int i = 1; i < argc; ++i)
+  for (int i = 1; i < argc; ++i) {
     if (std::strcmp(argv[i], "--gemm") == 0) return gemm_main(argc, argv);
+    if (std::strcmp(argv[i], "--issue") == 0) return issue_main();
+  }
   const int I = arg_int(argc, argv, "--input", 5), H = arg_int(argc, argv, "--hidden", 128);
   const int L = arg_int(argc, argv, "--layers", 4), O = arg_int(argc, argv, "--output", 24);
   const int B = arg_int(argc, argv, "--batch", 512), T = arg_int(argc, argv, "--seq", 1000);

@@ -570,4 +570,30 @@ int plh_probe_mfma_f16(double* tflops, double* clock_ghz) {
   return PLH_OK;
 }
 
+int plh_probe_issue_rates(double* cycles, int n) {
+  // (waves 0-3, waves 4-7) roles of the PLH_ISSUE_CASES cases, in the header's order
+  static const int kCases[PLH_ISSUE_CASES][2] = {{1, 0}, {2, 0}, {3, 0}, {1, 1}, {2, 2},
+                                                 {3, 3}, {1, 2}, {1, 3}, {4, 0}, {5, 0}};
+  if (!cycles || n < 2 * PLH_ISSUE_CASES) return fail(PLH_ERR_INVALID, "cycles needs 2 * PLH_ISSUE_CASES entries");
+  float* out = nullptr;
+  unsigned long long* cyc = nullptr;
+  unsigned long long h[2] = {0, 0};
+  hipError_t e = hipMalloc(&out, 512 * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&cyc, sizeof(h));
+  for (int c = 0; c < PLH_ISSUE_CASES && e == hipSuccess; ++c) {
+    for (int rep = 0; rep < 2 && e == hipSuccess; ++rep) {  // the first run warms the clock and caches
+      e = hipMemset(cyc, 0, sizeof(h));
+      if (e == hipSuccess) e = plh::launch_issue_probe(kCases[c][0], kCases[c][1], out, cyc, nullptr);
+      if (e == hipSuccess) e = hipMemcpy(h, cyc, sizeof(h), hipMemcpyDeviceToHost);
+    }
+    const double n_inst = plh::issue_probe_instructions();
+    cycles[2 * c] = (double)h[0] / n_inst;
+    cycles[2 * c + 1] = kCases[c][1] ? (double)h[1] / n_inst : 0.0;
+  }
+  if (out) (void)hipFree(out);
+  if (cyc) (void)hipFree(cyc);
+  if (e != hipSuccess) return fail_hip(e, "issue-rate probe");
+  return PLH_OK;
+}
+
 }  // extern "C"

@@ -60,14 +60,10 @@ __global__ void pack_rec_kernel(const _Float16* __restrict__ w_hh, int H, _Float
   dst[e] = (u < H && k < H) ? w_hh[((size_t)q * H + u) * H + k] : (_Float16)0.0f;
 }
 
-// Column of the input projection that lane `lane` of wave `wave` in slice `slice` reads as element
-// 2 q + j: gate q of unit slice * 64 + 8 wave + lane / 16 + 4 j.
-__host__ __device__ constexpr int rec_gate_col(int slice, int wave, int kgx) {
-  return ((slice * 8 + wave) * 4 + kgx) * 8;
-}
-
-// W_ih ([4H][K], torch layout) as the GEMM's W operand [4 HP][Kp] with rows in lane order (the
-// inverse of rec_gate_col), zero rows for padded units and zero columns K..Kp-1.
+// W_ih ([4H][K], torch layout) as the GEMM's W operand [4 HP][Kp] with rows in lane order: row
+// ((slice * 8 + wave) * 4 + kgx) * 8 + 2 q + j is gate q of unit slice * 64 + 8 wave + kgx + 4 j, the
+// element 2 q + j that lane kgx * 16 + en of that wave and slice reads from the projection; zero rows
+// for padded units and zero columns K..Kp-1.
 __global__ void pack_rec_wih_kernel(const _Float16* __restrict__ w_ih, int H, int HP, int K, int Kp,
                                     _Float16* __restrict__ dst) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -220,7 +216,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // X0: instead, x of step min(t, Tt - 1) as this lane's MFMA B fragment (row en, k 8 kgx .. +7) from
   // xp ([ntile][T][4][16] f16x8).
   // Blocked projections: step t's 16 rows of this tile are block row t * ntile + tile; this lane's
-  // 16 bytes are lane kgx * 16 + en of column block rec_gate_col(...) / 32 = slice * 8 + wave.
+  // 16 bytes are lane kgx * 16 + en of column block slice * 8 + wave (32 columns per block).
   const f16x8* gsrc = X0 ? nullptr
                          : reinterpret_cast<const f16x8*>(a.gates) + ((size_t)tile * (4 * HP / 32) + slice * 8 + wave) * 64 +
                                kgx * 16 + en;

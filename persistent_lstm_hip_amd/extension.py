@@ -74,6 +74,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plh_noalloc_scratch_bytes.argtypes = []
     lib.plh_probe_mfma_f16.restype = _i32
     lib.plh_probe_mfma_f16.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+    lib.plh_probe_issue_rates.restype = _i32
+    lib.plh_probe_issue_rates.argtypes = [ctypes.POINTER(ctypes.c_double), _i32]
     lib.plh_input_projection.restype = _i32
     lib.plh_input_projection.argtypes = [_vp, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp]
 
@@ -355,6 +357,19 @@ class NativeLibrary:
         ghz = ctypes.c_double(0.0)
         self._check(self.lib.plh_probe_mfma_f16(ctypes.byref(tf), ctypes.byref(ghz)), "plh_probe_mfma_f16")
         return float(tf.value), float(ghz.value)
+
+    ISSUE_CASES = ("mfma", "exp", "fma", "mfma|mfma", "exp|exp", "fma|fma", "mfma|exp", "mfma|fma",
+                   "mfma+fma", "mfma+exp")
+
+    def probe_issue_rates(self):
+        """{case: (cycles per instruction of waves 0-3, of waves 4-7 or None)} for the issue-rate
+        cases of plh_probe_issue_rates ("a|b": waves 0-3 issue a, waves 4-7 on the same SIMDs issue b;
+        "a+b": one wave issues both, figure per pair).  Synchronous, a few milliseconds."""
+        n = 2 * len(self.ISSUE_CASES)
+        buf = (ctypes.c_double * n)()
+        self._check(self.lib.plh_probe_issue_rates(buf, n), "plh_probe_issue_rates")
+        return {c: (float(buf[2 * i]), float(buf[2 * i + 1]) if "|" in c else None)
+                for i, c in enumerate(self.ISSUE_CASES)}
 
     # ---- the time-parallel input projection GEMM ---------------------------------------------
     def input_projection(self, x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None, *,

@@ -133,7 +133,8 @@ def input_projection_timing(ext, dev, reps: int = 20, warmup: int = 5) -> dict:
     """The time-parallel input-projection GEMM alone (fp16 MFMA, fp32 accumulation, fp16 result), in
     the fragment-blocked layout the layer-sequential path keeps, at the north star's input-GEMM shape
     [B*T, 128] x [128, 4*128] and at C4's layer shape [B*T, 512] x [512, 4*512]; HIP events on the
-    launch stream, median of `reps`."""
+    launch stream, median of `reps`.  Beside it, torch.mm on the same operands (row-major, W^T
+    contiguous): the vendor fp16 GEMM a caller would otherwise use, timed the same way."""
     res = []
     for M, K, N in ((B * T, 128, 512), (B * T, 512, 2048)):
         g = torch.Generator(device=dev).manual_seed(K)
@@ -150,16 +151,28 @@ def input_projection_timing(ext, dev, reps: int = 20, warmup: int = 5) -> dict:
             b.record()
         torch.cuda.synchronize()
         ms = statistics.median(a.elapsed_time(b) for a, b in ev)
+        wt = w.t().contiguous()
+        for _ in range(warmup):
+            torch.mm(x, wt, out=out)
+        torch.cuda.synchronize()
+        for a, b in ev:
+            a.record()
+            torch.mm(x, wt, out=out)
+            b.record()
+        torch.cuda.synchronize()
+        ms_vendor = statistics.median(a.elapsed_time(b) for a, b in ev)
         flops = 2.0 * M * N * K
         nbytes = 2.0 * (M * K + N * K + M * N)
         res.append({"shape": f"[{M},{K}]x[{K},{N}]", "ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
                     "frac_of_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
-                    "hbm_GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 8e12})
-        del x, w, out
+                    "hbm_GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 8e12,
+                    "torch_mm_ms": ms_vendor, "speedup_vs_torch_mm": ms_vendor / ms})
+        del x, w, wt, out
     torch.cuda.empty_cache()
     return {"kernel": "proj_gemm_kernel<true> (plh_gemm.hip)", "measured": res,
             "note": "timed alone with HIP events; C2 itself computes each step's projection inside the "
-                    "persistent wavefront kernel, C4 runs this GEMM for layers 1-3 (layer 0 in-kernel)"}
+                    "persistent wavefront kernel, C4 runs this GEMM for layers 1-3 (layer 0 in-kernel); "
+                    "torch_mm_ms: torch.mm on the same operands (row-major), timed the same way"}
 
 
 def uniform_batch_protocol(model, dev, warmup: int, steps: int) -> dict:

@@ -1,14 +1,15 @@
 #!/usr/bin/env python3
 """Headline benchmark: the stacked nn.LSTM + nn.Linear fp16 forward of BASELINE.json's metric.
 
-    python bench.py [--gpus 1] [--steps 100] [--warmup 10]
+    python bench.py [--gpus 1] [--steps 100] [--warmup 50]
     python bench.py --sweep [--cases 128:512,256:512,512:512]   # the reference's sweep CSV instead
 
 Workload (configs[1] of BASELINE.json, "C2"): 4-layer LSTM, input 5, hidden 128, Linear 128 -> 24,
 batch 512, seq 1000, fp16 weights/activations with fp32 accumulation, x ~ N(0, 1), PyTorch-default
 init from torch.manual_seed(42), h0 = c0 = 0.  A "step" is one full forward of that batch; inputs
-are resident in HBM before the timed region.  Timing follows the reference protocol
-(LSTM-hip.py:80-91: 10 warm-ups, 100 timed forwards) with HIP events.
+are resident in HBM before the timed region.  Timing: `--warmup` untimed forwards (default 50: the
+GPU's clock ramps up over a process's first ~30 launches of a recurrent kernel), then `--steps`
+timed forwards (default 100, as the reference's LSTM-hip.py:80-91) between two HIP events.
 
 Printed: one JSON line with the driver's fields plus
   roofline         -- the persistent kernel's algorithmic FLOPs per launch / its average duration
@@ -20,7 +21,9 @@ Printed: one JSON line with the driver's fields plus
                       star names), 1 warm-up + 3 timed forwards of the full C2 batch, median;
   cpu_reference_aten -- the reference's own ATen CPU path (persistent_lstm_reference.cpp:42-64,
                       compiled into oracle/_ref) timed the same way, when it is built;
-  parity           -- max/mean abs error of the GPU output against the torch fp32 CPU output.
+  parity           -- max/mean abs error of the GPU output against the torch fp32 CPU output;
+  dropin_route     -- the reference dispatcher's extension call (persistent_lstm4_forward_interleaved
+                      with kpairs weights) timed the same way, against the module's ms_per_step.
 """
 from __future__ import annotations
 
@@ -175,6 +178,49 @@ def input_projection_timing(ext, dev, reps: int = 20, warmup: int = 5) -> dict:
                     "torch_mm_ms: torch.mm on the same operands (row-major), timed the same way"}
 
 
+def _kpairs(w: torch.Tensor) -> torch.Tensor:
+    """The reference's kpairs weight format P[p, c, j] = W[c, 2p + j], zero-padded to even K
+    (model.py:20-27), restated here to feed its extension entry point."""
+    k = w.shape[1]
+    wt = torch.nn.functional.pad(w.t(), (0, 0, 0, k % 2))
+    return wt.reshape(-1, 2, w.shape[0]).permute(0, 2, 1).contiguous()
+
+
+def dropin_route_timing(native, x, warmup: int, steps: int, module_ms: float) -> dict:
+    """The reference dispatcher's per-forward call (model.py:584-656 calls
+    persistent_lstm_hip_ext.persistent_lstm4_forward_interleaved with kpairs-packed fp16 weights and
+    fp16 fused biases, model.py:548-578) served by this build's drop-in extension module: the same
+    protocol as the headline (warm-ups, then `steps` back-to-back calls between two events)."""
+    import persistent_lstm_hip_ext
+
+    lstm = native.lstm
+    dev = x.device
+    args = []
+    for l in range(L):
+        w_ih = getattr(lstm, f"weight_ih_l{l}").detach().to(dev, torch.float16)
+        w_hh = getattr(lstm, f"weight_hh_l{l}").detach().to(dev, torch.float16)
+        fused = (getattr(lstm, f"bias_ih_l{l}").detach().to(dev, torch.float16)
+                 + getattr(lstm, f"bias_hh_l{l}").detach().to(dev, torch.float16))
+        args += [_kpairs(w_ih), _kpairs(w_hh), fused]
+    args += [native.linear.weight.detach().to(dev, torch.float16), native.linear.bias.detach().to(dev, torch.float16)]
+    fwd = persistent_lstm_hip_ext.persistent_lstm4_forward_interleaved
+    with torch.inference_mode():
+        for _ in range(warmup):
+            fwd(x, *args)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(steps):
+            out = fwd(x, *args)
+        b.record()
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    return {"entry_point": "persistent_lstm_hip_ext.persistent_lstm4_forward_interleaved (kpairs weights, fp16 "
+                           "fused bias: the reference dispatcher's default C2 call)",
+            "ms_per_fwd": ms, "vs_module_ms_per_step": ms / module_ms, "steps": steps, "warmup": warmup,
+            "out_checksum": float(out.float().abs().sum())}
+
+
 def uniform_batch_protocol(model, dev, warmup: int, steps: int) -> dict:
     """The reference's own timing protocol (LSTM-hip.py:67-91): x = torch.ones(B, T, I), warm-ups, then
     100 timed forwards.  Both builds detect the uniform batch, compute one row and broadcast it
@@ -303,6 +349,7 @@ def main() -> int:
         torch.cuda.synchronize()
     # On-box check of the roofline constant (after the timed region): the dense fp16 MFMA rate this
     # GPU sustains with the kernels' instruction, and the shader clock meanwhile.
+    dropin = dropin_route_timing(native, x, args.warmup, args.steps, t_all0.elapsed_time(t_all1) / args.steps)
     probe_tflops, probe_ghz = ext.probe_mfma_f16()
     projection = input_projection_timing(ext, dev)
     uniform = uniform_batch_protocol(model, dev, args.warmup, args.steps)
@@ -373,6 +420,7 @@ def main() -> int:
             "latency_ratio": 30.8 / median_ms,
         },
         "uniform_batch": uniform,
+        "dropin_route": dropin,
         "other_configs": others,
     }
     if not args.no_cpu_baseline:

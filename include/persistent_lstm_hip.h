@@ -144,6 +144,10 @@ int plh_forward_noalloc(const void* packed_dev, int input_size, int hidden_size,
                         const void* c0, void* out, void* out_seq, void* h_n, void* c_n,
                         const int32_t* probe_steps, int n_probe, float* probe_h, float* probe_c, void* stream);
 int64_t plh_noalloc_scratch_bytes(void);
+/* plh_status for plh_forward_noalloc: synchronise `stream` and read the status word the last
+ * plh_forward_noalloc on the current device left in its scratch (0 = success, else PLH_STATUS_*
+ * bits).  Like the scratch, shared by every caller on that device.  No counterpart in the reference. */
+int plh_noalloc_status(uint32_t* status, void* stream);
 
 /* Synchronise `stream` and read the status word the last plh_forward left in `workspace`
  * (0 = success, else PLH_STATUS_* bits).  Returns PLH_OK or PLH_ERR_HIP. */
@@ -191,21 +195,6 @@ int plh_repeat_first_row(const void* in, void* out, int rows, int cols, void* st
  * allocates and frees its own buffers).  No counterpart in the reference, which quotes no peak.
  */
 int plh_probe_mfma_f16(double* tflops, double* clock_ghz);
-
-/*
- * Diagnostic for benchmarks: issue rates of one SIMD, in shader cycles per instruction of each
- * kind, from one workgroup of 8 waves (waves w and w + 4 share SIMD w), waves 0-3 in the first role
- * of a case and waves 4-7 in the second, each issuing 4096 instructions of its kind from 8
- * independent chains.  cycles[2 i] is case i's figure for wave 0, cycles[2 i + 1] for wave 4 (0 when
- * idle); n >= 2 * PLH_ISSUE_CASES.  Cases: 0 MFMA alone, 1 exp alone, 2 FMA alone, 3 MFMA | MFMA,
- * 4 exp | exp, 5 FMA | FMA, 6 MFMA | exp, 7 MFMA | FMA, 8 MFMA + FMA in one wave (per pair),
- * 9 MFMA + exp in one wave (per pair); MFMA = v_mfma_f32_16x16x32_f16, exp = v_exp_f32, FMA =
- * v_fma_f32.  They bound how far a step's gate math (exp, rcp and FMA-class VALU) can hide under the
- * MFMAs of the same or the other wave of its SIMD.  Runs on the current device's null stream
- * (allocates and frees its own buffers).  No counterpart in the reference.
- */
-#define PLH_ISSUE_CASES 10
-int plh_probe_issue_rates(double* cycles, int n);
 
 #ifdef __cplusplus
 }

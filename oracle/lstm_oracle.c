@@ -120,7 +120,9 @@ enum {
  * numerics: 0 = fp32 textbook, 1 = reference device numerics (see header), 2 = as 1 with the input
  *           projection W_ih x of every step rounded to fp16 before the bias and recurrent terms are
  *           added (the reference's generic path: persistent_lstm_hip.cu:2988-2994 computes it as an
- *           fp16 torch::matmul, the persistent kernel adds the rest in fp32).
+ *           fp16 torch::matmul, the persistent kernel adds the rest in fp32); 3 = as 2 for layers >= 1
+ *           only, layer 0's projection kept unrounded (the device's layer-sequential path with
+ *           input_size <= 32 computes layer 0's projection in fp32 inside its recurrent kernel).
  * Returns 0, or -1 for invalid arguments.
  */
 int oracle_lstm_forward(int B, int T, int I, int H, int L, const float* x, const float* const* w_ih,
@@ -185,7 +187,7 @@ int oracle_lstm_forward(int B, int T, int I, int H, int L, const float* x, const
               for (int k = 0; k < K; ++k) p += (double)wi[k] * (double)xt[k];
               /* numerics 2: the input projection is an fp16 tensor (the reference's generic path,
                  torch::matmul of fp16 operands, persistent_lstm_hip.cu:2988-2994) */
-              if (numerics == 2) p = (double)oracle_round_half((float)p);
+              if (numerics == 2 || (numerics == 3 && l > 0)) p = (double)oracle_round_half((float)p);
               double a = bl[g] + p;
               if (mutation != MUT_DROP_RECURRENT) {
                 if (mutation == MUT_TRANSPOSE_WHH) {

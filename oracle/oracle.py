@@ -11,6 +11,9 @@ Numerics modes (see the header of lstm_oracle.c for the reference file:line of e
   "ref_fp16_proj" -- as ref_fp16, with each step's input projection W_ih x rounded to fp16 before
                      the bias and recurrent terms are added (the reference's generic path, whose
                      projection is an fp16 torch::matmul).
+  "ref_fp16_proj_l1" -- as ref_fp16_proj for layers >= 1, layer 0's projection unrounded (this
+                     build's layer-sequential path with input_size <= 32, which projects layer 0
+                     inside its recurrent kernel in fp32 and the other layers with its fp16 GEMM).
 """
 from __future__ import annotations
 
@@ -122,7 +125,7 @@ def lstm_forward(
     [P,L,B,H] for probe_steps.
     """
     lib = _load()
-    mode = {"fp32": 0, "ref_fp16": 1, "ref_fp16_proj": 2}[numerics]
+    mode = {"fp32": 0, "ref_fp16": 1, "ref_fp16_proj": 2, "ref_fp16_proj_l1": 3}[numerics]
     x = _f32(x)
     if x.ndim != 3:
         raise ValueError("x must be [B, T, I]")
@@ -180,7 +183,7 @@ def linear(inp, w, b, numerics: str = "fp32") -> np.ndarray:
     """bias + inp w^T (double accumulation); "ref_fp16": operands rounded to fp16 and the result
     rounded to fp16 as the reference's head kernel does (persistent_lstm_hip.cu:1662-1682)."""
     lib = _load()
-    mode = {"fp32": 0, "ref_fp16": 1, "ref_fp16_proj": 1}[numerics]
+    mode = {"fp32": 0, "ref_fp16": 1, "ref_fp16_proj": 1, "ref_fp16_proj_l1": 1}[numerics]
     conv = round_half if mode == 1 else _f32
     inp, w = conv(inp), conv(w)
     b = conv(b) if b is not None else None

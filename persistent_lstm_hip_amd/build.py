@@ -60,8 +60,11 @@ def build(verbose: bool = False) -> str:
         print(out)
     os.replace(tmp, LIB_PATH)
     # Native driver of the C ABI (profiling target and integration example), linked to the library.
-    cmd = [hipcc(), "-O2", "-std=c++17", os.path.join(CSRC, "plh_bench_main.cpp"), "-L" + LIB_DIR,
-           "-lpersistent_lstm_hip", "-Wl,-rpath,$ORIGIN", "-o", BENCH_PATH + ".tmp"]
+    # (plh_issue_probe.hip: a developer probe kernel of plh_bench --issue, not part of the library.)
+    cmd = [hipcc(), "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "-Wno-unused-command-line-argument", os.path.join(CSRC, "plh_bench_main.cpp"),
+           os.path.join(CSRC, "plh_issue_probe.hip"), "-L" + LIB_DIR, "-lpersistent_lstm_hip", "-Wl,-rpath,$ORIGIN",
+           "-o", BENCH_PATH + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

@@ -15,8 +15,9 @@
 // known size, whose memory counters calibrate the forward's HBM traffic in a profiler.
 // --gemm K times plh_input_projection alone: [batch * seq, K] x [K, N] (N = --cols, default 4 K),
 // fragment-blocked by default (the layer-sequential path's layout), random fp16 operands.
-// --issue prints the SIMD issue rates of plh_probe_issue_rates (MFMA, v_exp_f32, v_fma_f32, alone,
-// beside each other in the two waves of a SIMD, and interleaved in one wave).
+// --issue prints the SIMD issue rates of MFMA, v_exp_f32 and v_fma_f32 (alone, beside each other in
+// the two waves of a SIMD, and interleaved in one wave), from a probe kernel of this program.
+// Every run releases what it created (buffers, events, stream) before it returns.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -135,32 +136,21 @@ int gemm_main(int argc, char** argv) {
   std::printf("{\"gemm\": [%lld, %d, %d], \"blocked\": %d, \"iters\": %d, \"ms\": %.6f, \"tflops\": %.3f}\n", M, K, N,
               blocked, iters, ms, flops / (ms * 1e-3) / 1e12);
   std::fflush(stdout);
+  HIP_OK(hipEventDestroy(e0));
+  HIP_OK(hipEventDestroy(e1));
+  HIP_OK(hipStreamDestroy(s));
+  for (void* p : {d_w, d_x, d_c}) HIP_OK(hipFree(p));
+  HIP_OK(hipDeviceSynchronize());
   return 0;
 }
 
-// --issue: the issue-rate table of plh_probe_issue_rates, one JSON line per case.
-int issue_main() {
-  static const char* kNames[PLH_ISSUE_CASES] = {"mfma",     "exp",      "fma",      "mfma|mfma", "exp|exp",
-                                                "fma|fma",  "mfma|exp", "mfma|fma", "mfma+fma",  "mfma+exp"};
-  double c[2 * PLH_ISSUE_CASES];
-  if (plh_probe_issue_rates(c, 2 * PLH_ISSUE_CASES) != PLH_OK) {
-    std::fprintf(stderr, "plh_probe_issue_rates: %s\n", plh_last_error());
-    return 1;
-  }
-  for (int i = 0; i < PLH_ISSUE_CASES; ++i) {
-    if (std::strchr(kNames[i], '|'))
-      std::printf("{\"case\": \"%s\", \"cycles_per_inst_waves_0_3\": %.2f, \"cycles_per_inst_waves_4_7\": %.2f}\n",
-                  kNames[i], c[2 * i], c[2 * i + 1]);
-    else
-      std::printf("{\"case\": \"%s\", \"cycles_per_inst_waves_0_3\": %.2f}\n", kNames[i], c[2 * i]);
-  }
-  return 0;
-}
+// --issue: SIMD issue rates (plh_issue_probe.hip, built into this program only).
+int plh_bench_issue_rates();
 
 int main(int argc, char** argv) {
   for (int i = 1; i < argc; ++i) {
     if (std::strcmp(argv[i], "--gemm") == 0) return gemm_main(argc, argv);
-    if (std::strcmp(argv[i], "--issue") == 0) return issue_main();
+    if (std::strcmp(argv[i], "--issue") == 0) return plh_bench_issue_rates();
   }
   const int I = arg_int(argc, argv, "--input", 5), H = arg_int(argc, argv, "--hidden", 128);
   const int L = arg_int(argc, argv, "--layers", 4), O = arg_int(argc, argv, "--output", 24);
@@ -254,6 +244,14 @@ int main(int argc, char** argv) {
       "{\"geometry\": [%d, %d, %d, %d], \"batch\": %d, \"seq\": %d, \"iters\": %d, \"fwd_ms\": %.6f, "
       "\"kernel_ms\": %.6f, \"seq_steps_per_s\": %.6e, \"status\": %u, \"abs_checksum\": %.6f}\n",
       I, H, L, O, B, T, iters, fwd_ms, kern_ms, seq_steps / (fwd_ms * 1e-3), status, checksum);
-  std::fflush(stdout);  // profilers may end the process abnormally after main returns
+  std::fflush(stdout);
+  HIP_OK(hipEventDestroy(e0));
+  HIP_OK(hipEventDestroy(e1));
+  HIP_OK(hipStreamDestroy(s));
+  for (int l = 0; l < L; ++l)
+    for (void* p : {w_ih[l], w_hh[l], b_ih[l], b_hh[l]}) HIP_OK(hipFree(p));
+  for (void* p : {d_lw, d_lb, d_x, packed, ws, out}) HIP_OK(hipFree(p));
+  if (d_len) HIP_OK(hipFree(d_len));
+  HIP_OK(hipDeviceSynchronize());
   return status == 0 ? 0 : 2;
 }

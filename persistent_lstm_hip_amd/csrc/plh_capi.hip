@@ -439,6 +439,7 @@ int plh_forward_noalloc(const void* packed_dev, int input_size, int hidden_size,
                         const void* x, int batch, int seq_len, const int32_t* lengths, const void* h0, const void* c0,
                         void* out, void* out_seq, void* h_n, void* c_n, const int32_t* probe_steps, int n_probe,
                         float* probe_h, float* probe_c, void* stream) {
+  if (batch < 0 || seq_len < 0) return fail(PLH_ERR_INVALID, "batch and seq_len must be non-negative");
   const int64_t need = plh_workspace_bytes(input_size, hidden_size, num_layers, output_size, batch, seq_len);
   if (need < 0) return geometry_code(input_size, hidden_size, num_layers, output_size);
   if ((uint64_t)need > kScratchBytes)
@@ -454,6 +455,14 @@ int plh_forward_noalloc(const void* packed_dev, int input_size, int hidden_size,
 }
 
 int64_t plh_noalloc_scratch_bytes(void) { return (int64_t)kScratchBytes; }
+
+int plh_noalloc_status(uint32_t* status, void* stream) {
+  if (!status) return fail(PLH_ERR_INVALID, "status is required");
+  hipError_t err = hipSuccess;
+  void* ws = scratch_ptr(&err);
+  if (!ws) return fail_hip(err, "scratch symbol lookup");
+  return plh_status(ws, status, stream);  // the status word opens the workspace plh_forward lays out there
+}
 
 int plh_kernel_timing(int max_forwards) {
   KernelTiming& tm = timing();
@@ -567,32 +576,6 @@ int plh_probe_mfma_f16(double* tflops, double* clock_ghz) {
   }
   *tflops = ms > 0.f ? plh::mfma_probe_flops(blocks, iters) / (ms * 1e-3) / 1e12 : 0.0;
   *clock_ghz = ticks > 0.0 ? cycles / (ticks * 10.0) : 0.0;  // 100 MHz ticks: 10 ns each
-  return PLH_OK;
-}
-
-int plh_probe_issue_rates(double* cycles, int n) {
-  // (waves 0-3, waves 4-7) roles of the PLH_ISSUE_CASES cases, in the header's order
-  static const int kCases[PLH_ISSUE_CASES][2] = {{1, 0}, {2, 0}, {3, 0}, {1, 1}, {2, 2},
-                                                 {3, 3}, {1, 2}, {1, 3}, {4, 0}, {5, 0}};
-  if (!cycles || n < 2 * PLH_ISSUE_CASES) return fail(PLH_ERR_INVALID, "cycles needs 2 * PLH_ISSUE_CASES entries");
-  float* out = nullptr;
-  unsigned long long* cyc = nullptr;
-  unsigned long long h[2] = {0, 0};
-  hipError_t e = hipMalloc(&out, 512 * sizeof(float));
-  if (e == hipSuccess) e = hipMalloc(&cyc, sizeof(h));
-  for (int c = 0; c < PLH_ISSUE_CASES && e == hipSuccess; ++c) {
-    for (int rep = 0; rep < 2 && e == hipSuccess; ++rep) {  // the first run warms the clock and caches
-      e = hipMemset(cyc, 0, sizeof(h));
-      if (e == hipSuccess) e = plh::launch_issue_probe(kCases[c][0], kCases[c][1], out, cyc, nullptr);
-      if (e == hipSuccess) e = hipMemcpy(h, cyc, sizeof(h), hipMemcpyDeviceToHost);
-    }
-    const double n_inst = plh::issue_probe_instructions();
-    cycles[2 * c] = (double)h[0] / n_inst;
-    cycles[2 * c + 1] = kCases[c][1] ? (double)h[1] / n_inst : 0.0;
-  }
-  if (out) (void)hipFree(out);
-  if (cyc) (void)hipFree(cyc);
-  if (e != hipSuccess) return fail_hip(e, "issue-rate probe");
   return PLH_OK;
 }
 

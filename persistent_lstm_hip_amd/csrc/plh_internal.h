@@ -144,7 +144,7 @@ hipError_t launch_forward_prologue(const Geometry& g, const ForwardArgs& a, uint
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t s);
 hipError_t launch_repeat_first_row(const _Float16* in, _Float16* out, int rows, int cols, hipStream_t s);
 
-// Persistent kernels (device function pointers for hipLaunchCooperativeKernel), nullptr if no variant
+// Persistent kernels (device function pointers for hipLaunchKernel), nullptr if no variant
 // exists: the wavefront kernel for padded H <= 128 and 8- or 16-row tiles (plh_wavefront.hip), the
 // sliced kernel for padded H 256 / 512 with 1 or 2 tiles per workgroup (plh_sliced.hip).
 const void* wavefront_kernel(int HP, int tile_rows, bool ragged);
@@ -185,11 +185,6 @@ double proj_gemm_flops(long long M, int N, int K);
 // iters x 8 independent v_mfma_f32_16x16x32_f16; out holds blocks x 1024 floats, clk blocks x 2
 // (shader cycles, 100 MHz ticks of the loop).  mfma_probe_flops: the FLOPs of one launch.
 hipError_t launch_mfma_probe(int blocks, int iters, float* out, unsigned long long* clk, hipStream_t s);
-// One workgroup of 8 waves: waves 0-3 run role ra, 4-7 role rb (0 idle, 1 MFMA, 2 exp, 3 FMA,
-// 4 MFMA + FMA, 5 MFMA + exp), issue_probe_instructions() each; cyc[0], cyc[1]: shader cycles of
-// waves 0 and 4.
-hipError_t launch_issue_probe(int ra, int rb, float* out, unsigned long long* cyc, hipStream_t s);
-int issue_probe_instructions();
 double mfma_probe_flops(int blocks, int iters);
 
 }  // namespace plh

@@ -1,5 +1,5 @@
 // plh_launch.hip -- host side of the kernels: geometry rules, buffer layouts, kernel choice,
-// occupancy and the cooperative launch of the persistent recurrence.
+// occupancy and the launch of the persistent recurrence.
 #include "plh_device.h"
 
 namespace plh {
@@ -145,7 +145,16 @@ hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t
   void* params[] = {&args};
   // One layer per launch (layer-sequential) or every layer of the chunk at once.
   const unsigned grid = g.rec ? a.ntile * g.slices : a.L * a.ntile / a.wg_tiles * g.slices;
-  return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(g.waves * 64), params, 0, s);
+  // An ordinary launch on the stream's own queue.  Co-residency of the grid comes from the caller:
+  // plh_forward sizes every launch to at most the occupancy-derived capacity (recurrent_capacity),
+  // and the launch starts after the stream's previous kernels have finished, so every workgroup is
+  // dispatched at once; the kernels' waits are bounded, so a workgroup that were not resident would
+  // end the launch with PLH_STATUS_TIMEOUT and NaN outputs, not a hang.  The kernels use no
+  // grid-wide barrier.  (A cooperative launch, used before, ran each persistent kernel on a second
+  // HSA queue of the runtime: ~11 us per hop between the two queues in kernel traces, twice per
+  // forward, and that extra queue was the one runtime object of forward runs that GEMM-only runs
+  // never created.)
+  return hipLaunchKernel(fn, dim3(grid), dim3(g.waves * 64), params, 0, s);
 }
 
 }  // namespace plh

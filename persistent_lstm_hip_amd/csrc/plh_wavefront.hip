@@ -1,6 +1,6 @@
 // plh_wavefront.hip -- the persistent layer-wavefront kernel (H <= 128) of the stacked LSTM +
-// Linear inference forward on CDNA4 (gfx950).  Cooperative launch: every workgroup is co-resident
-// and loops over the time steps itself.
+// Linear inference forward on CDNA4 (gfx950).  Every workgroup of a launch is co-resident (the host
+// sizes the grid to the device's occupancy) and loops over the time steps itself.
 //
 // One workgroup per (layer, batch tile of 8 or 16 rows):
 //   * each wave owns 16 hidden units and keeps the i, f, g, o rows of [W_ih | W_hh] for them in

@@ -72,10 +72,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     )
     lib.plh_noalloc_scratch_bytes.restype = _i64
     lib.plh_noalloc_scratch_bytes.argtypes = []
+    lib.plh_noalloc_status.restype = _i32
+    lib.plh_noalloc_status.argtypes = [ctypes.POINTER(ctypes.c_uint32), _vp]
     lib.plh_probe_mfma_f16.restype = _i32
     lib.plh_probe_mfma_f16.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
-    lib.plh_probe_issue_rates.restype = _i32
-    lib.plh_probe_issue_rates.argtypes = [ctypes.POINTER(ctypes.c_double), _i32]
     lib.plh_input_projection.restype = _i32
     lib.plh_input_projection.argtypes = [_vp, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp]
 
@@ -358,19 +358,6 @@ class NativeLibrary:
         self._check(self.lib.plh_probe_mfma_f16(ctypes.byref(tf), ctypes.byref(ghz)), "plh_probe_mfma_f16")
         return float(tf.value), float(ghz.value)
 
-    ISSUE_CASES = ("mfma", "exp", "fma", "mfma|mfma", "exp|exp", "fma|fma", "mfma|exp", "mfma|fma",
-                   "mfma+fma", "mfma+exp")
-
-    def probe_issue_rates(self):
-        """{case: (cycles per instruction of waves 0-3, of waves 4-7 or None)} for the issue-rate
-        cases of plh_probe_issue_rates ("a|b": waves 0-3 issue a, waves 4-7 on the same SIMDs issue b;
-        "a+b": one wave issues both, figure per pair).  Synchronous, a few milliseconds."""
-        n = 2 * len(self.ISSUE_CASES)
-        buf = (ctypes.c_double * n)()
-        self._check(self.lib.plh_probe_issue_rates(buf, n), "plh_probe_issue_rates")
-        return {c: (float(buf[2 * i]), float(buf[2 * i + 1]) if "|" in c else None)
-                for i, c in enumerate(self.ISSUE_CASES)}
-
     # ---- the time-parallel input projection GEMM ---------------------------------------------
     def input_projection(self, x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None, *,
                          blocked: bool = False) -> torch.Tensor:
@@ -439,34 +426,39 @@ class NativeLibrary:
         self._check(rc, "plh_repeat_first_row")
         return out
 
-    def _packed_for(self, w_ih: Sequence[torch.Tensor], w_hh: Sequence[torch.Tensor], bias: Sequence[torch.Tensor],
-                    linear_weight: torch.Tensor, linear_bias: Optional[torch.Tensor], source: tuple) -> torch.Tensor:
-        """Packed weights for torch-layout parameters, cached on the identity and version of the
-        tensors the caller passed (`source`): the reference's dispatcher passes the same cached
-        tensors to every forward (model.py:542-582), so they are packed once per weight version."""
+    def _packed_for(self, source: tuple, make_weights) -> tuple:
+        """(packed blob, dims) for reference-format arguments, cached on the identity and version of
+        the tensors the caller passed (`source`): the reference's dispatcher passes the same cached
+        tensors to every forward (model.py:542-582), so they are converted and packed once per weight
+        version.  make_weights() -> (w_ih list, w_hh list, fused bias list, linear weight, linear
+        bias) in torch layout; it runs only on a cache miss, so a hit launches nothing but the
+        forward."""
         from .model import _TensorSetKey  # noqa: PLC0415 (model imports this module)
 
         key = getattr(self, "_compat_key", None)
         if key is None or not key.matches(source):
+            w_ih, w_hh, bias, linear_weight, linear_bias = make_weights()
+            if not (len(w_ih) == len(w_hh) == len(bias)) or not w_ih:
+                raise ValueError("weight_ih, weight_hh and bias need one tensor per layer")
             self._compat_blob = self.pack(w_ih, w_hh, bias, None, linear_weight, linear_bias)
+            self._compat_dims = (int(w_ih[0].shape[1]), int(w_hh[0].shape[1]), len(w_ih),
+                                 int(linear_weight.shape[0]))
             self._compat_key = _TensorSetKey(source)
-        return self._compat_blob
+        return self._compat_blob, self._compat_dims
 
     def persistent_lstm_regressor_forward_generic_projected(
         self, x, weight_ih: List[torch.Tensor], weight_hh: List[torch.Tensor], bias: List[torch.Tensor],
         linear_weight: torch.Tensor, linear_bias: torch.Tensor,
     ) -> torch.Tensor:
         """bindings.cpp:163: (x, [W_ih], [W_hh], [b_ih + b_hh], W_lin, b_lin) -> [B, O]."""
-        return self._forward_torch_layout(x, list(weight_ih), list(weight_hh), list(bias), linear_weight, linear_bias,
-                                          tuple(weight_ih) + tuple(weight_hh) + tuple(bias) + (linear_weight, linear_bias))
+        source = tuple(weight_ih) + tuple(weight_hh) + tuple(bias) + (linear_weight, linear_bias)
+        return self._forward_reference_format(
+            x, source, lambda: (list(weight_ih), list(weight_hh), list(bias), linear_weight, linear_bias))
 
-    def _forward_torch_layout(self, x, w_ih, w_hh, bias, linear_weight, linear_bias, source) -> torch.Tensor:
+    def _forward_reference_format(self, x, source: tuple, make_weights) -> torch.Tensor:
         if not isinstance(x, torch.Tensor) or x.dim() != 3:
             raise ValueError("x must be a [batch, seq_len, input_size] tensor")
-        if not (len(w_ih) == len(w_hh) == len(bias)) or not w_ih:
-            raise ValueError("weight_ih, weight_hh and bias need one tensor per layer")
-        packed = self._packed_for(w_ih, w_hh, bias, linear_weight, linear_bias, source)
-        dims = (int(w_ih[0].shape[1]), int(w_hh[0].shape[1]), len(w_ih), int(linear_weight.shape[0]))
+        packed, dims = self._packed_for(source, make_weights)
         return self.forward(packed, dims, x)["out"]
 
     @staticmethod
@@ -488,25 +480,27 @@ class NativeLibrary:
     def persistent_lstm4_forward(self, x, *args) -> torch.Tensor:
         """bindings.cpp:155: torch-layout weights [4H, K] and fused biases, 4 layers."""
         self._four_layers(args)
-        return self._forward_torch_layout(x, [args[3 * l] for l in range(4)], [args[3 * l + 1] for l in range(4)],
-                                          [args[3 * l + 2] for l in range(4)], args[12], args[13], args)
+        return self._forward_reference_format(
+            x, args, lambda: ([args[3 * l] for l in range(4)], [args[3 * l + 1] for l in range(4)],
+                              [args[3 * l + 2] for l in range(4)], args[12], args[13]))
 
     def persistent_lstm4_forward_packed(self, x, *args) -> torch.Tensor:
         """bindings.cpp:156: transposed weights W^T [K, 4H] (persistent_lstm_hip.cu:2005-2018) and fused
         biases, 4 layers."""
         self._four_layers(args)
-        return self._forward_torch_layout(x, [args[3 * l].t() for l in range(4)], [args[3 * l + 1].t() for l in range(4)],
-                                          [args[3 * l + 2] for l in range(4)], args[12], args[13], args)
+        return self._forward_reference_format(
+            x, args, lambda: ([args[3 * l].t() for l in range(4)], [args[3 * l + 1].t() for l in range(4)],
+                              [args[3 * l + 2] for l in range(4)], args[12], args[13]))
 
     def persistent_lstm4_forward_interleaved(self, x, *args) -> torch.Tensor:
         """bindings.cpp:157: kpairs-packed W_ih and W_hh (model.py:562-578) and fused biases."""
         self._four_layers(args)
         H = int(args[1].size(1)) // 4
-        I = int(x.size(2))
-        return self._forward_torch_layout(
-            x, [self.unpack_kpairs(args[3 * l], I if l == 0 else H) for l in range(4)],
-            [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)], [args[3 * l + 2] for l in range(4)],
-            args[12], args[13], args)
+        I = int(x.size(2)) if isinstance(x, torch.Tensor) and x.dim() == 3 else 0
+        return self._forward_reference_format(
+            x, args, lambda: ([self.unpack_kpairs(args[3 * l], I if l == 0 else H) for l in range(4)],
+                              [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)],
+                              [args[3 * l + 2] for l in range(4)], args[12], args[13]))
 
     def persistent_lstm4_forward_monolithic(self, x, *args) -> torch.Tensor:
         """bindings.cpp:162: the interleaved arguments (the reference's all-layers-in-one-kernel variant,
@@ -517,9 +511,10 @@ class NativeLibrary:
         """bindings.cpp:158: native W_ih [4H, K] with kpairs-packed W_hh (model.py:548-560)."""
         self._four_layers(args)
         H = int(args[0].size(0)) // 4
-        return self._forward_torch_layout(
-            x, [args[3 * l] for l in range(4)], [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)],
-            [args[3 * l + 2] for l in range(4)], args[12], args[13], args)
+        return self._forward_reference_format(
+            x, args, lambda: ([args[3 * l] for l in range(4)],
+                              [self.unpack_kpairs(args[3 * l + 1], H) for l in range(4)],
+                              [args[3 * l + 2] for l in range(4)], args[12], args[13]))
 
     def persistent_lstm4_forward_projected_uniform(self, x, virtual_batch_size: int, *args) -> torch.Tensor:
         """bindings.cpp:159: the projected arguments for ONE sequence x [1, T, I] -> [1, O] (the caller

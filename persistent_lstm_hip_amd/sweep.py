@@ -27,30 +27,28 @@ columns (compare_lstm_sweeps.py:46-87):
 from __future__ import annotations
 
 import argparse
-import csv
 import os
+import re
 import sys
 import time
-from dataclasses import dataclass
-from io import StringIO
 from statistics import median
-from typing import Dict, List, Sequence, Tuple
+from typing import Dict, Iterable, List, NamedTuple, Sequence, Tuple
 
 SUMMARY_HEADER = "hidden,batch,seq,elapsed_s,throughput,kernel"
 COMPARE_HEADER = ("hidden,batch,seq,native_elapsed,adaptive_elapsed,elapsed_speedup,native_tput,adaptive_tput,"
                   "tput_speedup,kernel")
 NATIVE_KERNEL = "native_pytorch_lstm"
 
+Shape = Tuple[int, int, int]  # (hidden, batch, seq): the key that joins two sweeps
 
-@dataclass(frozen=True)
-class ShapeCase:
+
+class ShapeCase(NamedTuple):
     hidden: int
     batch: int
     seq: int
 
 
-@dataclass(frozen=True)
-class SweepRow:
+class SweepRow(NamedTuple):
     hidden: int
     batch: int
     seq: int
@@ -58,75 +56,81 @@ class SweepRow:
     throughput: float
     kernel: str
 
+    @property
+    def shape(self) -> Shape:
+        return (self.hidden, self.batch, self.seq)
+
+    def csv(self) -> str:
+        return f"{self.hidden},{self.batch},{self.seq},{self.elapsed_s:.6f},{self.throughput:.3f},{self.kernel}"
+
+
+# "hidden:batch" or "hidden:batch:seq", decimal integers, blanks around the item allowed.
+_CASE = re.compile(r"\s*(\d+):(\d+)(?::(\d+))?\s*")
+# One summary record: three integers, two numbers and the (possibly empty) kernel name.
+_RECORD = re.compile(r"(\d+),(\d+),(\d+),([-+.\deE]+|nan|inf),([-+.\deE]+|nan|inf),([^,]*)")
+
 
 def parse_cases(raw: str, default_seq: int) -> List[ShapeCase]:
-    """'128:512,256:512:300' -> cases; a missing seq is default_seq (run_native_lstm_sweep.py:35-52)."""
-    cases: List[ShapeCase] = []
-    for piece in raw.split(","):
-        piece = piece.strip()
-        if not piece:
-            continue
-        parts = piece.split(":")
-        if len(parts) not in (2, 3):
-            raise ValueError("cases must look like 128:512,256:512,512:128 or hidden:batch:seq")
-        hidden, batch = int(parts[0]), int(parts[1])
-        seq = int(parts[2]) if len(parts) == 3 else default_seq
-        if hidden <= 0 or batch <= 0 or seq <= 0:
-            raise ValueError(f"case {piece!r}: hidden, batch and seq must be positive")
-        cases.append(ShapeCase(hidden, batch, seq))
-    if not cases:
+    """'128:512,256:512:300' -> cases (the sweep's case syntax, run_native_lstm_sweep.py:35-52); a
+    missing seq is default_seq; empty items are skipped."""
+    items = [item for item in raw.split(",") if item.strip()]
+    if not items:
         raise ValueError("no sweep cases given")
+    cases = []
+    for item in items:
+        m = _CASE.fullmatch(item)
+        if m is None:
+            raise ValueError(f"case {item.strip()!r}: expected hidden:batch or hidden:batch:seq "
+                             "(e.g. 128:512,256:512,512:128)")
+        case = ShapeCase(int(m[1]), int(m[2]), int(m[3]) if m[3] is not None else default_seq)
+        if min(case) <= 0:
+            raise ValueError(f"case {item.strip()!r}: hidden, batch and seq must be positive")
+        cases.append(case)
     return cases
 
 
-def format_summary(rows: Sequence[SweepRow]) -> str:
-    lines = [SUMMARY_HEADER]
-    for r in rows:
-        lines.append(f"{r.hidden},{r.batch},{r.seq},{r.elapsed_s:.6f},{r.throughput:.3f},{r.kernel}")
-    return "\n".join(lines)
+def format_summary(rows: Iterable[SweepRow]) -> str:
+    return "\n".join([SUMMARY_HEADER] + [r.csv() for r in rows])
 
 
-def extract_csv_block(text: str) -> str:
-    """The last summary block of a sweep output (compare_lstm_sweeps.py:28-43)."""
-    lines = text.splitlines()
-    header_idx = -1
-    for idx, line in enumerate(lines):
-        if line.strip().startswith("hidden,batch,seq,elapsed_s,throughput"):
-            header_idx = idx
-    if header_idx < 0:
-        raise ValueError("could not find sweep summary CSV header")
-    block: List[str] = []
-    for line in lines[header_idx:]:
-        stripped = line.strip()
-        if not stripped:
+def read_summary(text: str) -> Dict[Shape, SweepRow]:
+    """The rows of the last summary block of a sweep output (the block starts at a line holding the
+    summary header and runs over the record lines right after it), keyed by shape; a later row of
+    one shape replaces an earlier one.  ValueError if the text holds no header."""
+    lines = [line.strip() for line in text.splitlines()]
+    starts = [i for i, line in enumerate(lines) if line.startswith(SUMMARY_HEADER.rsplit(",", 1)[0])]
+    if not starts:
+        raise ValueError("no sweep summary block (header 'hidden,batch,seq,elapsed_s,throughput,...') found")
+    table: Dict[Shape, SweepRow] = {}
+    for line in lines[starts[-1] + 1:]:
+        m = _RECORD.fullmatch(line)
+        if m is None:
             break
-        if stripped.startswith("hidden,") or stripped[0].isdigit():
-            block.append(stripped)
-    return "\n".join(block)
+        row = SweepRow(int(m[1]), int(m[2]), int(m[3]), float(m[4]), float(m[5]), m[6])
+        table[row.shape] = row
+    return table
 
 
-def parse_rows(text: str) -> Dict[Tuple[int, int, int], SweepRow]:
-    rows: Dict[Tuple[int, int, int], SweepRow] = {}
-    for raw in csv.DictReader(StringIO(extract_csv_block(text))):
-        key = (int(raw["hidden"]), int(raw["batch"]), int(raw["seq"]))
-        rows[key] = SweepRow(*key, elapsed_s=float(raw["elapsed_s"]), throughput=float(raw["throughput"]),
-                             kernel=raw.get("kernel") or "")
-    return rows
+# A summary of this build may be compared as either side; the joined line's kernel column names the
+# second ("adaptive") sweep's kernel, as compare_lstm_sweeps.py:77-87 prints it.
+def join_sweeps(base: Dict[Shape, SweepRow], other: Dict[Shape, SweepRow]) -> List[Tuple[SweepRow, SweepRow]]:
+    """(base row, other row) for every shape both sweeps measured, in shape order."""
+    return [(base[k], other[k]) for k in sorted(base.keys() & other.keys())]
 
 
 def compare(native_text: str, adaptive_text: str) -> str:
-    """Joined rows of two sweep outputs (compare_lstm_sweeps.py:64-87): elapsed speedup = native /
-    other elapsed, throughput speedup = other / native throughput, kernel of the other sweep."""
-    native, other = parse_rows(native_text), parse_rows(adaptive_text)
-    common = sorted(set(native) & set(other))
-    if not common:
+    """compare_lstm_sweeps.py's joined table of two sweep outputs: elapsed speedup = base elapsed /
+    other elapsed, throughput speedup = other / base throughput."""
+    pairs = join_sweeps(read_summary(native_text), read_summary(adaptive_text))
+    if not pairs:
         raise ValueError("no common hidden,batch,seq rows found")
-    lines = [COMPARE_HEADER]
-    for key in common:
-        n, a = native[key], other[key]
-        lines.append(f"{a.hidden},{a.batch},{a.seq},{n.elapsed_s:.6f},{a.elapsed_s:.6f},{n.elapsed_s / a.elapsed_s:.3f},"
-                     f"{n.throughput:.3f},{a.throughput:.3f},{a.throughput / n.throughput:.3f},{a.kernel}")
-    return "\n".join(lines)
+    out = [COMPARE_HEADER]
+    for base, other in pairs:
+        fields = [str(v) for v in other.shape]
+        fields += [f"{base.elapsed_s:.6f}", f"{other.elapsed_s:.6f}", f"{base.elapsed_s / other.elapsed_s:.3f}"]
+        fields += [f"{base.throughput:.3f}", f"{other.throughput:.3f}", f"{other.throughput / base.throughput:.3f}"]
+        out.append(",".join(fields + [other.kernel]))
+    return "\n".join(out)
 
 
 def _env_int(name: str, default: int) -> int:

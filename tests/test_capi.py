@@ -175,13 +175,6 @@ def test_mfma_probe_validates_before_touching_the_device(ext):
     assert b"required" in ext.lib.plh_last_error()
 
 
-def test_issue_probe_validates_before_touching_the_device(ext):
-    assert ext.lib.plh_probe_issue_rates(None, 0) == PLH_ERR_INVALID
-    assert b"PLH_ISSUE_CASES" in ext.lib.plh_last_error()
-    buf = (ctypes.c_double * 4)()
-    assert ext.lib.plh_probe_issue_rates(buf, 4) == PLH_ERR_INVALID
-
-
 def test_kernel_timing_arming_without_forwards(ext):
     assert ext.lib.plh_kernel_timing(0) == PLH_OK
     ms, n = ext.kernel_timing_read()

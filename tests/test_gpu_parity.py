@@ -567,25 +567,6 @@ def test_mfma_rate_probe(gpu):
     assert 1000.0 < tflops < 3000.0, tflops
 
 
-def test_issue_rate_probe(gpu):
-    """The SIMD issue rates behind the step analysis: one v_mfma_f32_16x16x32_f16 per ~16 shader
-    cycles from one wave, the two waves of a SIMD sharing the matrix core (the later one takes about
-    twice as long), two waves' FMAs issued side by side, and an exp slower than an FMA."""
-    _say("issue-rate probe")
-    r = gpu.probe_issue_rates()
-    assert set(r) == set(gpu.ISSUE_CASES)
-    for case, (a, b) in r.items():
-        assert np.isfinite(a) and a > 0.0, (case, a)
-        assert (b is None) == ("|" not in case), (case, b)
-        if b is not None:
-            assert np.isfinite(b) and b > 0.0, (case, b)
-    mfma, fma, exp = r["mfma"][0], r["fma"][0], r["exp"][0]
-    assert 14.0 < mfma < 22.0, mfma
-    assert max(r["mfma|mfma"]) > 1.6 * mfma, r["mfma|mfma"]
-    assert max(r["fma|fma"]) < 1.4 * fma, (r["fma|fma"], fma)
-    assert exp > fma, (exp, fma)
-
-
 def test_random_geometry_sweep(gpu):
     """Seeded random geometries through plh_forward: input size, hidden size (both kernel families,
     padded and unpadded), layers, head size (0 = no head), batch, length, ragged lengths with zeros,

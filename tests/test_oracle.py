@@ -215,6 +215,28 @@ def test_ref_fp16_modes_match_stepwise_torch_emulation(mode):
     assert np.abs(other["c_n"][0] - c.numpy()).max() > 1e-5, "the two modes must differ measurably"
 
 
+def test_ref_fp16_proj_l1_rounds_only_the_hidden_layers_projections():
+    """numerics='ref_fp16_proj_l1' (layer 0's projection unrounded, layers >= 1 rounded): layer 0 is
+    exactly ref_fp16's layer 0, and layer 1 is exactly a one-layer ref_fp16_proj run over layer 0's
+    fp16 output sequence."""
+    I, H, B, T = 7, 24, 3, 30
+    lstm = _torch_lstm(I, H, 2, seed=23)
+    x = make_x(B, T, I).numpy()
+    layers = [tuple(getattr(lstm, f"{n}_l{l}").detach().numpy() for n in ("weight_ih", "weight_hh", "bias_ih",
+                                                                            "bias_hh")) for l in range(2)]
+    both = oracle.lstm_forward(x, layers, numerics="ref_fp16_proj_l1", probe_steps=(1, T))
+    first = oracle.lstm_forward(x, layers[:1], numerics="ref_fp16", probe_steps=(1, T), want_seq=True)
+    np.testing.assert_array_equal(both["probe_h"][:, 0], first["probe_h"][:, 0])
+    np.testing.assert_array_equal(both["probe_c"][:, 0], first["probe_c"][:, 0])
+    second = oracle.lstm_forward(first["out_seq"], layers[1:], numerics="ref_fp16_proj", probe_steps=(1, T))
+    np.testing.assert_array_equal(both["probe_h"][:, 1], second["probe_h"][:, 0])
+    np.testing.assert_array_equal(both["probe_c"][:, 1], second["probe_c"][:, 0])
+    # and it is neither of the uniform modes
+    for other in ("ref_fp16", "ref_fp16_proj"):
+        r = oracle.lstm_forward(x, layers, numerics=other, probe_steps=(1, T))
+        assert not np.array_equal(r["probe_c"], both["probe_c"]), other
+
+
 def test_linear_modes_match_float64():
     """oracle.linear: fp32 mode = float64 product rounded to float32; ref_fp16 = operands rounded to
     fp16, float64 product rounded through float32 to fp16 (the reference head's fp16 output)."""

@@ -33,7 +33,8 @@ hidden,batch,seq,elapsed_s,throughput,kernel
 def test_parse_cases():
     cases = sweep.parse_cases("128:512, 256:512:300,", default_seq=1000)
     assert cases == [sweep.ShapeCase(128, 512, 1000), sweep.ShapeCase(256, 512, 300)]
-    for bad in ("128", "128:512:1:2", "", "0:5"):
+    assert sweep.parse_cases(" 64:8 ", default_seq=7) == [sweep.ShapeCase(64, 8, 7)]
+    for bad in ("128", "128:512:1:2", "", "0:5", "a:b", "12:-3", ",,"):
         with pytest.raises(ValueError):
             sweep.parse_cases(bad, 1000)
 
@@ -43,16 +44,37 @@ def test_summary_round_trip():
             sweep.SweepRow(512, 64, 50, 1.5, 4266.6666, "k2")]
     text = "noise\n" + sweep.format_summary(rows) + "\n\ntrailing"
     assert text.splitlines()[1] == sweep.SUMMARY_HEADER
-    back = sweep.parse_rows(text)
+    back = sweep.read_summary(text)
     assert back[(128, 512, 1000)] == sweep.SweepRow(128, 512, 1000, 0.088123, 581034.457, "k1")
     assert back[(512, 64, 50)].kernel == "k2"
 
 
 def test_extract_uses_the_last_summary_block():
     text = NATIVE_OUT + "\nsummary:\n" + sweep.SUMMARY_HEADER + "\n64,8,10,1.000000,80.000,late\n"
-    assert set(sweep.parse_rows(text)) == {(64, 8, 10)}
+    assert set(sweep.read_summary(text)) == {(64, 8, 10)}
     with pytest.raises(ValueError):
-        sweep.parse_rows("no csv here")
+        sweep.read_summary("no csv here")
+
+
+def test_summary_block_ends_at_the_first_non_record_line():
+    text = (sweep.SUMMARY_HEADER + "\n  128,512,1000,1.5,2.5,k  \n256,8,10,1e-3,4E+2,\nnot a record\n"
+            "512,1,1,1.0,1.0,after\n")
+    rows = sweep.read_summary(text)
+    assert set(rows) == {(128, 512, 1000), (256, 8, 10)}
+    assert rows[(256, 8, 10)] == sweep.SweepRow(256, 8, 10, 1e-3, 400.0, "")
+    # a header with nothing after it is an empty table, and a repeated shape keeps its last row
+    assert sweep.read_summary("x\n" + sweep.SUMMARY_HEADER) == {}
+    dup = sweep.SUMMARY_HEADER + "\n1,2,3,1.0,1.0,a\n1,2,3,2.0,2.0,b\n"
+    assert sweep.read_summary(dup)[(1, 2, 3)].kernel == "b"
+
+
+def test_join_sweeps_in_shape_order():
+    a = sweep.read_summary(NATIVE_OUT)
+    b = sweep.read_summary(HIP_OUT)
+    pairs = sweep.join_sweeps(a, b)
+    assert [p[0].shape for p in pairs] == [(128, 512, 1000), (512, 128, 1000)]
+    assert all(x.shape == y.shape for x, y in pairs)
+    assert sweep.join_sweeps(a, {}) == []
 
 
 def test_compare_joins_common_rows():
@@ -86,6 +108,6 @@ def test_run_hip_prints_a_parsable_summary():
     buf = io.StringIO()
     rows = sweep.run([sweep.ShapeCase(64, 16, 20), sweep.ShapeCase(200, 8, 10)], iters=3, warmup=1, out=buf)
     assert [(r.hidden, r.batch, r.seq) for r in rows] == [(64, 16, 20), (200, 8, 10)]
-    parsed = sweep.parse_rows(buf.getvalue())
+    parsed = sweep.read_summary(buf.getvalue())
     assert parsed[(64, 16, 20)].kernel == "hip_mi355x_persistent_wavefront" and parsed[(64, 16, 20)].throughput > 0
     assert torch.cuda.is_available()

@@ -5,6 +5,8 @@ second smaller (it then runs on scratch still holding the first call's data); an
 forward that needs more scratch than it holds."""
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -19,6 +21,13 @@ PLH_ERR_INVALID = 1
 
 def _say(msg):
     print(f"[gpu-case] {msg}", flush=True)
+
+
+def _noalloc_status(gpu):
+    st = ctypes.c_uint32(0xFFFFFFFF)
+    rc = gpu.lib.plh_noalloc_status(ctypes.byref(st), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, gpu.last_error()
+    return st.value
 
 
 def _noalloc(gpu, blob, dims, x, probes, outs):
@@ -50,7 +59,7 @@ def test_noalloc_matches_plh_forward_twice(gpu, first, second):
         outs = {k: torch.full_like(v, 7.0) for k, v in ref.items()}
         rc = _noalloc(gpu, blob, (I, H, L, O), xd, probes, outs)
         assert rc == 0, gpu.last_error()
-        gpu.check_status(torch.device("cuda"))
+        assert _noalloc_status(gpu) == 0, "the noalloc forward's own status word reports a failed wait"
         torch.cuda.synchronize()
         for k in ref:
             assert torch.equal(outs[k], ref[k]), f"{k} differs from plh_forward"
@@ -77,3 +86,12 @@ def test_noalloc_rejects_a_forward_larger_than_its_scratch(gpu):
     assert "MiB of device scratch" in gpu.last_error()
     torch.cuda.synchronize()
     assert (outs["out"] == 7.0).all(), "nothing may be launched for a rejected forward"
+
+
+def test_noalloc_rejects_negative_sizes(gpu):
+    _say("noalloc negative sizes")
+    for B, T in ((-1, 10), (4, -1)):
+        rc = gpu.lib.plh_forward_noalloc(None, 5, 128, 4, 24, None, B, T, None, None, None, None, None, None, None,
+                                         None, 0, None, None, None)
+        assert rc == PLH_ERR_INVALID, (B, T, rc)
+        assert "non-negative" in gpu.last_error()

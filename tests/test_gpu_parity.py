@@ -255,13 +255,13 @@ def test_large_batches_use_16_row_tiles_and_split_launches(gpu, B, T):
     assert_close(got.float().cpu().numpy()[rows], ref, what=f"B={B} vs oracle")
 
 
-@pytest.mark.parametrize("H,rows_checked", [(256, 512), (512, 48)])
-def test_large_hidden_c3_c4(gpu, H, rows_checked):
+@pytest.mark.parametrize("H", [256, 512])
+def test_large_hidden_c3_c4(gpu, H):
     """C3 (H256) and C4 (H512): 4 layers, B512, T1000.  C3 runs the sliced kernel (two tiles per
     workgroup), C4 the layer-sequential path (one 512-row launch per layer).
 
-    Output vs torch fp32 on `rows_checked` rows spread over every launch; h and c after 1, 100 and
-    1000 steps vs the oracle on rows of the first and the last launch.
+    Output vs torch fp32 on all 512 rows; h and c of every layer after 1, 100 and 1000 steps vs the
+    oracle on 32 rows spread over the batch (every tile group and both ends).
     """
     I, L, O, B, T = 5, 4, 24, 512, 1000
     _say(f"large hidden H={H} B={B} T={T}")
@@ -270,18 +270,47 @@ def test_large_hidden_c3_c4(gpu, H, rows_checked):
     model = _gpu_model(native)
     out, ph, pc = model.forward_probe(x.to("cuda", torch.float16), [1, 100, 1000])
     gpu.check_status(torch.device("cuda"))
-    rows = np.arange(B) if rows_checked >= B else np.linspace(0, B - 1, rows_checked).astype(int)
-    want = _torch_ref(native, x[rows])
-    mx, mn = assert_close(out.float().cpu().numpy()[rows], want, what=f"H={H} out vs torch fp32")
+    want = _torch_ref(native, x)
+    mx, mn = assert_close(out.float().cpu().numpy(), want, what=f"H={H} out vs torch fp32 (all {B} rows)")
     _say(f"H={H} out vs torch fp32: max_abs={mx:.3e} mean_abs={mn:.3e}")
-    nprobe = 8 if H <= 256 else 4  # the scalar oracle takes ~1.5 s per row at H512
-    prow = np.r_[0:nprobe, B - nprobe:B]
+    prow = np.unique(np.r_[0:4, np.linspace(4, B - 5, 24).astype(int), B - 4:B])
+    assert prow.size >= 32
     ref = oracle.lstm_forward(x.numpy()[prow], oracle_layers(native.lstm), probe_steps=(1, 100, 1000))
     for p, step in enumerate((1, 100, 1000)):
         for name, got_all, want_all in (("h", ph, ref["probe_h"]), ("c", pc, ref["probe_c"])):
             g = got_all[p][:, prow].cpu().numpy()
             mx, mn = assert_close(g, want_all[p], what=f"H={H} {name} after {step} steps")
             _say(f"H={H} {name}@{step}: max_abs={mx:.3e} mean_abs={mn:.3e}")
+
+
+def test_h512_row_pinned_on_both_paths(gpu):
+    """At padded H 512 the batch size picks the path (L = 4: B <= 256 the all-layers sliced kernel,
+    whose projections stay fp32; B > 256 the layer-sequential path, whose GEMM projections of layers
+    1-3 are fp16).  The same rows at B = 256 and B = 320 are each pinned to the oracle's restatement
+    of their own rounding (ref_fp16 / ref_fp16_proj_l1) with the regression bounds, and both to the
+    fp32 oracle at the north-star tolerance."""
+    I, H, L, O, T = 5, 512, 4, 24, 300
+    native = make_regressor(I, H, L, O)
+    model = _gpu_model(native)
+    x = make_x(320, T, I)
+    rows = np.r_[0:6, 250:256]
+    layers = oracle_layers(native.lstm)
+    lw, lb = linear_params(native.linear)
+    want32 = oracle.regressor_forward(x.numpy()[rows], layers, lw, lb)
+    got = {}
+    for B, numerics in ((256, "ref_fp16"), (320, "ref_fp16_proj_l1")):
+        _say(f"H512 pinned rows at B={B} ({numerics})")
+        out, ph, pc = model.forward_probe(x[:B].to("cuda", torch.float16), [T])
+        gpu.check_status(torch.device("cuda"))
+        got[B] = out.float().cpu().numpy()[rows]
+        ref = oracle.lstm_forward(x.numpy()[rows], layers, numerics=numerics, probe_steps=(T,))
+        head = oracle.linear(ref["h_n"][-1], lw, lb, numerics="ref_fp16")
+        mx, mn = assert_close(got[B], head, max_abs=2e-4, mean_abs=2e-5, what=f"B={B} head vs {numerics}")
+        _say(f"B={B} head vs {numerics}: max_abs {mx:.2e}")
+        for name, g, w in (("h", ph, ref["probe_h"]), ("c", pc, ref["probe_c"])):
+            assert_close(g[0][:, rows].cpu().numpy(), w[0], max_abs=4e-4, mean_abs=4e-5, what=f"B={B} {name}")
+        assert_close(got[B], want32, what=f"B={B} head vs fp32 oracle")
+    assert not np.array_equal(got[256], got[320]), "the two paths are expected to round differently"
 
 
 def test_sliced_persistent_lstm_dropin_with_state(gpu):

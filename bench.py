@@ -242,14 +242,16 @@ def uniform_batch_protocol(model, dev, warmup: int, steps: int) -> dict:
 
 
 def other_configs(dev, reps: int = 20, warmup: int = 10) -> dict:
-    """C3, C4 and C5 (BASELINE.json configs[2..4]) timed the same way as C2 (HIP events, median of
-    `reps` forwards after `warmup` untimed ones, so the clock has settled after the previous
-    config) on their own synthetic models: parity for these is in
+    """C3, C4 and C5 (BASELINE.json configs[2..4]), and H = 1024 (the largest hidden size the
+    reference's generic entry point serves; 4 layers, batch 512, seq 1000), timed the same way as C2
+    (HIP events, median of `reps` forwards after `warmup` untimed ones, so the clock has settled
+    after the previous config) on their own synthetic models: parity for these is in
     tests/test_gpu_parity.py; here only their latency and seq-steps/s are recorded."""
     from persistent_lstm_hip_amd import PersistentLSTMRegressor, StandardLSTMRegressor
 
     res = {}
-    for name, hid, ragged in (("C3_H256", 256, False), ("C4_H512", 512, False), ("C5_ragged_H128", 128, True)):
+    for name, hid, ragged in (("C3_H256", 256, False), ("C4_H512", 512, False), ("C5_ragged_H128", 128, True),
+                              ("H1024", 1024, False)):
         torch.manual_seed(42)
         native = StandardLSTMRegressor(I, hid, O, L).eval()
         model = PersistentLSTMRegressor.from_native_module(native).to(dev).half().eval()

@@ -47,7 +47,9 @@ int plh_abi_version(void);
 /* Message describing the last error raised on the calling thread ("" if none). */
 const char* plh_last_error(void);
 
-/* 1 if plh_forward implements this geometry, else 0 (plh_last_error() says why).
+/* 1 if plh_forward implements this geometry, else 0 (plh_last_error() says why): 1 <= H <= 1024, any
+ * input size up to 65536, L <= 64, O <= 4096 (the reference's generic entry point serves
+ * 1 <= H <= 1024 and any input size, model.py:154-165, persistent_lstm_hip.cu:2981-2991).
  * Replaces the shape predicates PersistentLSTMRegressor._can_use_specialized_regressor_hip
  * (model.py:432-441) and NativeModuleFallback._can_use_generic_projected_module (model.py:131-165). */
 int plh_supports(int input_size, int hidden_size, int num_layers, int output_size);
@@ -90,13 +92,14 @@ int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int
  *             probe_h / probe_c device fp32 [n_probe, L, batch, H] receive every layer's state
  *             after that many steps (h as rounded to fp16, c in fp32).  n_probe = 0: no probes.
  *   workspace device memory of at least plh_workspace_bytes(...) bytes, 256-byte aligned.
- * Any output pointer may be NULL.  Asynchronous on `stream`.  At padded H 512, a batch that needs
- * more wavefront launches than there are layers runs layer by layer instead: per layer the input
- * projection of every step as one fp16 MFMA GEMM (plh_input_projection's kernel; for layer 0 with
- * input_size <= 32 inside the recurrent kernel), then a W_hh-only persistent kernel.  That path
- * rounds x_t W_ih^T to fp16 before the recurrent sum, as the reference's generic path does
- * (persistent_lstm_hip.cu:2988-2994); the all-layers path keeps it in fp32, so at padded H 512 the
- * batch size decides which of the two roundings a row gets (both are within the tolerance).
+ * Any output pointer may be NULL.  Asynchronous on `stream`.  Hidden sizes 513..1024, inputs wider
+ * than the padded hidden size, and at padded H 512 a batch that needs more wavefront launches than
+ * there are layers run layer by layer: per layer the input projection of every step as one fp16
+ * MFMA GEMM (plh_input_projection's kernel; for layer 0 with input_size <= 32 at H > 256 inside the
+ * recurrent kernel), then a W_hh-only persistent kernel.  That path rounds the GEMM's x_t W_ih^T to
+ * fp16 before the recurrent sum, as the reference's generic path does (persistent_lstm_hip.cu:
+ * 2988-2994); the all-layers path keeps it in fp32, so at padded H 512 the batch size decides which
+ * of the two roundings a row gets (both are within the tolerance).
  * Replaces persistent_lstm4_forward_interleaved (bindings.cpp:157, persistent_lstm_hip.cu:2126-2254)
  * and persistent_lstm_regressor_forward_generic_projected (bindings.cpp:163,
  * persistent_lstm_hip.cu:2923-3181), whose signatures return only the [batch, O] head output;
@@ -118,7 +121,7 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
  *            (((r / 16) * (ld / 32) + c / 32) * 64 + ((c % 32) / 8) * 16 + r % 16) * 8 + c % 8, so that
  *            every 16 rows x 32 columns are one contiguous 1 KB block (the layout of the
  *            layer-sequential path's layer inputs and projections; the faster form)
- * Requires k % 128 == 0, k <= 512, cols % 128 == 0, ldx >= k and ldo >= cols multiples of 8
+ * Requires k % 128 == 0, k <= 65536, cols % 128 == 0, ldx >= k and ldo >= cols multiples of 8
  * (blocked: of 32, and rows % 16 == 0), 16-byte aligned pointers (PLH_ERR_INVALID otherwise;
  * zero-pad K to meet them).  Asynchronous on `stream`.
  * Replaces the reference's torch::matmul input projections of fp16 tensors (the generic path's

@@ -109,6 +109,12 @@ Plan plan_path(const plh::Geometry& g, int batch, bool need_device, hipError_t* 
 // projections for every step, ~4 MB per step at 512 rows - stays within kMaxSeqWorkspace.
 constexpr size_t kMaxSeqWorkspace = (size_t)24 << 30;
 Plan plan_for(const plh::Geometry& g, int batch, int seq_len, bool need_device, hipError_t* err) {
+  if (!g.wave_ok) {
+    // Padded H 1024, or an input wider than the padded H: only the layer-sequential path exists.
+    Plan q = plan_path(plh::as_layer_sequential(g), batch, need_device, err);
+    q.rec = true;
+    return q;
+  }
   const Plan p = plan_path(g, batch, need_device, err);
   if (!g.rec_ok || *err != hipSuccess) return p;
   const plh::Geometry gr = plh::as_layer_sequential(g);
@@ -243,9 +249,12 @@ int plh_pack_regressor(int input_size, int hidden_size, int num_layers, int outp
   size_t wih_off = p.wih;
   for (int l = 0; l < g.L; ++l) {
     if (!w_ih[l] || !w_hh[l]) return fail(PLH_ERR_INVALID, "null weight pointer for layer " + std::to_string(l));
-    hipError_t e = plh::launch_pack_layer(g, l, (const _Float16*)w_ih[l], (const _Float16*)w_hh[l],
-                                          (_Float16*)(base + p.wpack), s);
-    if (e != hipSuccess) return fail_hip(e, "pack_layer launch");
+    hipError_t e = hipSuccess;
+    if (g.wave_ok) {
+      e = plh::launch_pack_layer(g, l, (const _Float16*)w_ih[l], (const _Float16*)w_hh[l],
+                                 (_Float16*)(base + p.wpack), s);
+      if (e != hipSuccess) return fail_hip(e, "pack_layer launch");
+    }
     if (g.rec_ok) {
       // The layer-sequential path's operands: W_hh fragments; W_ih as the projection GEMM's W operand,
       // or for layer 0 with I <= 32 as the recurrent kernel's MFMA fragments.
@@ -388,8 +397,11 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
         err = hipEventRecord(tm.ev[2 * tm.used], s);
         if (err != hipSuccess) return fail_hip(err, "timing event");
       }
+      // x for layer 0's GEMM: in xs slot 0, or (input wider than the padded H) in its own buffer
+      _Float16* const xin = g.kp0 > g.HP ? (_Float16*)(ws + w.xin) : xs[0];
+      const int ld0 = g.kp0 > g.HP ? g.kp0 : g.HP;
       if (!g.rec_x0) {
-        err = plh::launch_rec_input(g, a, xs[0], s);
+        err = plh::launch_rec_input(g, a, xin, ld0, s);
         if (err != hipSuccess) return fail_hip(err, "input transpose");
       }
       const _Float16* wih = (const _Float16*)(pk + p.wih);
@@ -398,8 +410,8 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
         const bool x0 = l == 0 && g.rec_x0;
         if (!x0) {
           const int Kp = l == 0 ? g.kp0 : g.kp;
-          err = plh::launch_proj_gemm(xs[l & 1], g.HP, wih, Kp, gates, 4 * g.HP, (long long)seq_len * a.rows_pad,
-                                      4 * g.HP, true, cus, s);
+          err = plh::launch_proj_gemm(l == 0 ? xin : xs[l & 1], l == 0 ? ld0 : g.HP, wih, Kp, gates, 4 * g.HP,
+                                      (long long)seq_len * a.rows_pad, 4 * g.HP, true, cus, s);
           if (err != hipSuccess) return fail_hip(err, "input projection GEMM launch");
           wih += (size_t)4 * g.HP * Kp;
         }
@@ -500,8 +512,9 @@ int plh_input_projection(const void* x, int64_t ldx, const void* w, int k, void*
                          int cols, int blocked, void* stream) {
   if (blocked != 0 && blocked != 1) return fail(PLH_ERR_INVALID, "blocked must be 0 or 1");
   if (!plh::gemm_shape_ok(rows, cols, k, ldx, ldo, blocked != 0))
-    return fail(PLH_ERR_INVALID, "plh_input_projection needs rows >= 0, cols % 128 == 0, k % 128 == 0, k <= 512, "
-                                 "ldx >= k and ldo >= cols (multiples of 8; blocked: of 32, rows % 16 == 0)");
+    return fail(PLH_ERR_INVALID, "plh_input_projection needs rows >= 0, cols % 128 == 0, k % 128 == 0, "
+                                 "k <= 65536, ldx >= k and ldo >= cols (multiples of 8; blocked: of 32, "
+                                 "rows % 16 == 0)");
   if (rows > 0 && (!x || !w || !out)) return fail(PLH_ERR_INVALID, "x, w and out are required");
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16))
     return fail(PLH_ERR_INVALID, "x, w and out must be 16-byte aligned");

@@ -128,19 +128,30 @@ struct Sliced {
   static_assert(HP == 256 || HP == 512, "padded H 256 or 512");
 };
 
-// Work split of the layer-sequential recurrent kernel (padded H = 512, plh_rec.hip): the input
-// projection comes precomputed, so a workgroup holds only W_hh rows, for HS = 64 hidden units, and
-// S = 8 workgroups serve a 16-row tile.  Wave w serves units 8 w .. 8 w + 7 of the slice over all
-// of K (16 K-chunks of 32 x 2 tiles of 16 gate rows = 128 VGPRs).
+// Work split of the layer-sequential recurrent kernel (plh_rec.hip): the input projection comes
+// precomputed, so a workgroup holds only W_hh rows, for HS hidden units, and S workgroups
+// ("slices") serve a 16-row tile.  Wave w serves the 4 NJ units 4 NJ w .. + 4 NJ - 1 of its slice
+// over all of K as NJ MFMA A tiles of 16 gate rows (row r of tile j: gate r % 4 of unit
+// 4 NJ w + 4 j + r / 4), KCH K-chunks of 32 each, i.e. KCH NJ fragments (4 VGPRs each):
+//   HP     NJ  HS  S   fragments per wave
+//   128    2   64  2   8
+//   256    2   64  4   16
+//   512    2   64  8   32  (128 VGPRs)
+//   1024   1   32  32  32  (128 VGPRs; 32 slices = the 32 CUs of one XCD per tile)
 template <int HP>
 struct Rec {
-  static constexpr int kS = 8;            // workgroups per 16-row tile
-  static constexpr int kHs = HP / kS;     // hidden units per workgroup
+  static constexpr int kNj = HP == 1024 ? 1 : 2;  // A tiles (4-unit groups) per wave
+  static constexpr int kUpw = 4 * kNj;    // hidden units per wave
+  static constexpr int kHs = 8 * kUpw;    // hidden units per workgroup
+  static constexpr int kS = HP / kHs;     // workgroups per 16-row tile
   static constexpr int kKch = HP / 32;    // K chunks of h
   static constexpr int kWords = HP * 8;   // ring words reserved per step slot of a tile (the packed
                                           // words of one step take half)
-  static_assert(kHs == 64, "four 16-unit groups per workgroup");
+  static_assert(HP == 128 || HP == 256 || HP == 512 || HP == 1024, "padded H of the layer-sequential path");
+  static_assert(kS * kHs == HP && kS >= 2 && kS <= 32, "slices");
 };
+// Rec<HP>::kS for a runtime padded H (host side).
+inline int rec_slices(int HP) { return HP == 1024 ? 32 : HP / 64; }
 
 // ---- tagged exchange of h among the workgroups of a tile (plh_sliced.hip; plh_rec.hip shares
 // sliced_coords and packs its words itself) ----

@@ -8,9 +8,11 @@
 // reference's per-layer torch::matmul of fp16 tensors (persistent_lstm_hip.cu:2988-2994, fp16
 // result), written as a hand-written MFMA kernel instead of a library GEMM.
 //
-// Design (K <= 512, so a 128-column slice of W is at most 128 KB):
+// Design (a 128-column slice of W over 512 K is 128 KB of LDS):
 //   * weight-stationary: each workgroup owns one 128-column slice of W, loaded once into LDS in MFMA
-//     fragment order, and walks the 512-row m-tiles of its m-group; its 8 waves (two per SIMD) each
+//     fragment order when K <= 512 (for K > 512 the slice is held in K blocks of 512, reloaded in
+//     turn for every m-tile between two barriers), and walks the 512-row m-tiles of its m-group; its
+//     8 waves (two per SIMD) each
 //     compute a 64 (m) x 128 (n) sub-tile with v_mfma_f32_16x16x32_f16 (4 x 8 accumulator tiles,
 //     128 fp32 per lane), W as the MFMA's A operand and X as its B operand;
 //   * X goes from global memory straight into the B-fragment registers (a lane's 8 consecutive k
@@ -30,9 +32,9 @@
 //     16 bytes then sit at lane * 16 of a 1 KB block, so every load and store instruction of a wave
 //     moves 1 KB of whole cache lines (row-major: 16 rows x 64 B).  The layer-sequential path keeps
 //     its layer inputs and projections blocked (the recurrent kernel writes and reads them so).
-// Requirements (checked by the host): K % 128 == 0, K <= 512, N % 128 == 0, ldx and ldc multiples
-// of 8 (blocked: of 32, and M % 16 == 0), 16-byte aligned pointers.  Rows m >= M are not stored
-// (their loads are clamped to row M - 1).
+// Requirements (checked by the host): K % 128 == 0, K <= kGemmMaxKTotal, N % 128 == 0, ldx and ldc
+// multiples of 8 (blocked: of 32, and M % 16 == 0), 16-byte aligned pointers.  Rows m >= M are not
+// stored (their loads are clamped to row M - 1).
 #include <algorithm>
 
 #include "plh_device.h"
@@ -51,6 +53,7 @@ constexpr int kGemmWM = 32 / kGemmWaves;              // 16-row m-tiles per wave
 constexpr int kGemmBM = kGemmWaves * kGemmWM * 16;    // rows per m-tile of a workgroup (512)
 constexpr int kGemmBN = 128;                          // columns per workgroup (its W slice)
 constexpr int kGemmMaxK = 512;                        // W slice of 128 x 512 fp16 = 128 KB of LDS
+constexpr int kGemmKbSteps = kGemmMaxK / 32;          // k-steps of one K block
 constexpr int kRing = PLH_GEMM_RING;                  // X fragment ring depth (k-steps of 32)
 constexpr int kGemmKStep = 32 * kRing;                // K granule
 constexpr int kGemmThreads = kGemmWaves * 64;
@@ -60,12 +63,13 @@ __device__ __forceinline__ int gemm_w_row(int nt, int i) {
   return 32 * (nt >> 1) + 8 * (i >> 2) + 4 * (nt & 1) + (i & 3);
 }
 
-template <bool BLK>
+// KB: K > 512, the W slice held in K blocks of 512 (kGemmKbSteps k-steps) reloaded per m-tile.
+template <bool BLK, bool KB>
 __global__ void __launch_bounds__(kGemmThreads)
 proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* __restrict__ W, int K,
                  _Float16* __restrict__ C, long long ldc, int M, int tiles_m, int n_slices, int m_groups) {
   constexpr int WM = kGemmWM;
-  // W slice: [k-chunk of 32][n-tile 0..7][64 lanes] f16x8, k-chunk major.
+  // W slice (or K block of it): [k-chunk of 32][n-tile 0..7][64 lanes] f16x8, k-chunk major.
   __shared__ f16x8 wl[kGemmMaxK / 32 * 8 * 64];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -77,13 +81,20 @@ proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* 
   const int n0 = ns * kGemmBN;
   const int KS = K / 32;  // k-steps per tile (a multiple of kRing)
 
-  // The W slice into LDS (once).
-  for (int e = threadIdx.x; e < KS * 8 * 64; e += kGemmThreads) {
-    const int l = e & 63, nt = (e >> 6) & 7, kc = e >> 9;
-    const int n = n0 + gemm_w_row(nt, l & 15);
-    wl[e] = *reinterpret_cast<const f16x8*>(W + (size_t)n * K + kc * 32 + (l >> 4) * 8);
+  // K block kb of the W slice (k-steps 16 kb .. 16 kb + 15, fewer in a last partial block) into LDS.
+  auto load_w = [&](int kb) {
+    const int ks0 = kb * kGemmKbSteps;
+    const int nks = KS - ks0 < kGemmKbSteps ? KS - ks0 : kGemmKbSteps;
+    for (int e = threadIdx.x; e < nks * 8 * 64; e += kGemmThreads) {
+      const int l = e & 63, nt = (e >> 6) & 7, kc = e >> 9;
+      const int n = n0 + gemm_w_row(nt, l & 15);
+      wl[e] = *reinterpret_cast<const f16x8*>(W + (size_t)n * K + (ks0 + kc) * 32 + (l >> 4) * 8);
+    }
+  };
+  if constexpr (!KB) {
+    load_w(0);  // the whole slice, once
+    __syncthreads();
   }
-  __syncthreads();
 
   // m-tiles of this m-group: mg, mg + m_groups, ...
   int mt = mg;
@@ -121,6 +132,15 @@ proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* 
 #pragma unroll
       for (int b = 0; b < 8; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int kq = 0; kq < KS; kq += kRing) {
+      if constexpr (KB) {
+        // A new K block of W: every wave is done with the previous one (its MFMAs read it from
+        // registers loaded before them), then the block is loaded and visible to all.
+        if (kq % kGemmKbSteps == 0) {
+          __syncthreads();
+          load_w(kq / kGemmKbSteps);
+          __syncthreads();
+        }
+      }
 #pragma unroll
       for (int j = 0; j < kRing; ++j) {
         // Prefetch flat step + kRing - 1 into its slot: this tile's k-step kq + j + kRing - 1, or the
@@ -132,7 +152,7 @@ proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* 
 #pragma unroll
           for (int a = 0; a < WM; ++a) xr[(j + kRing - 1) % kRing][a] = xptr(t, a)[kk * kStepVec];
         }
-        const f16x8* wp = wl + (kq + j) * 8 * 64 + lane;
+        const f16x8* wp = wl + (KB ? (kq + j) % kGemmKbSteps : kq + j) * 8 * 64 + lane;
         f16x8 wa[8];
 #pragma unroll
         for (int b = 0; b < 8; ++b) wa[b] = wp[b * 64];
@@ -175,7 +195,7 @@ proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* 
 
 bool gemm_shape_ok(long long M, int N, int K, long long ldx, long long ldc, bool blocked) {
   const int q = blocked ? 32 : 8;
-  return M >= 0 && N > 0 && K > 0 && N % kGemmBN == 0 && K % kGemmKStep == 0 && K <= kGemmMaxK && ldx >= K &&
+  return M >= 0 && N > 0 && K > 0 && N % kGemmBN == 0 && K % kGemmKStep == 0 && K <= kGemmMaxKTotal && ldx >= K &&
          ldc >= N && ldx % q == 0 && ldc % q == 0 && (!blocked || M % 16 == 0) && M <= (long long)INT32_MAX;
 }
 
@@ -188,12 +208,11 @@ hipError_t launch_proj_gemm(const _Float16* X, long long ldx, const _Float16* W,
   // m-tile), placed so that an m-group's slices share an XCD.
   const int m_groups = std::max(1, std::min(tiles_m, std::max(cus, 1) / n_slices));
   const int grid = ((m_groups + 7) / 8) * 8 * n_slices;
-  if (blocked)
-    hipLaunchKernelGGL(proj_gemm_kernel<true>, dim3(grid), dim3(kGemmThreads), 0, s, X, ldx, W, K, C, ldc, (int)M,
-                       tiles_m, n_slices, m_groups);
-  else
-    hipLaunchKernelGGL(proj_gemm_kernel<false>, dim3(grid), dim3(kGemmThreads), 0, s, X, ldx, W, K, C, ldc, (int)M,
-                       tiles_m, n_slices, m_groups);
+  const bool kb = K > kGemmMaxK;
+  auto* fn = blocked ? (kb ? proj_gemm_kernel<true, true> : proj_gemm_kernel<true, false>)
+                     : (kb ? proj_gemm_kernel<false, true> : proj_gemm_kernel<false, false>);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(kGemmThreads), 0, s, X, ldx, W, K, C, ldc, (int)M, tiles_m, n_slices,
+                     m_groups);
   return hipGetLastError();
 }
 

@@ -17,10 +17,12 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 // i = f = o = 0.5, g = 0 and their c and h stay exactly 0: padding never changes real outputs.
 struct Geometry {
   int I, H, L, O;
-  int HP;      // padded hidden size: 32, 64, 128 (one workgroup per layer and tile), 256 (sliced) or
-               // 512 (layer-sequential)
-  int slices;  // workgroups per (layer, tile): 1, 4 (HP = 256), 16 (HP = 512) or 8 (layer-sequential)
-  int rec_ok;  // HP = 512: the layer-sequential path exists (its weights are packed too)
+  int HP;      // padded hidden size: 32, 64, 128 (one workgroup per layer and tile), 256, 512 (sliced)
+               // or 1024 (layer-sequential only); 128 at least when I > HP
+  int slices;  // workgroups per (layer, tile): 1, 4 (HP = 256), 16 (HP = 512); on the layer-sequential
+               // path Rec<HP>::kS (2, 4, 8, 32)
+  int wave_ok;  // the all-layers kernels serve this geometry (HP <= 512 and I <= HP)
+  int rec_ok;  // the layer-sequential path serves it (HP >= 512, or I > HP): its weights are packed too
   int rec;     // this forward runs layer by layer: input projection as a GEMM, recurrent kernel
                // holding W_hh alone (make_geometry leaves 0; as_layer_sequential sets it)
   int max_wg_tiles;  // 16-row tiles a sliced workgroup can carry (2 at HP = 256, software-pipelined)
@@ -33,6 +35,8 @@ struct Geometry {
                // recurrent kernel (one MFMA K chunk); otherwise by the projection GEMM like the others
   int kp0, kp;  // K of the projection GEMM, padded to a multiple of 128: layer 0 (0 with rec_x0), layers >= 1
 };
+// The layer-sequential path's padded hidden sizes and the largest hidden size served.
+constexpr int kMaxHidden = 1024;
 
 // u32 words per (layer, tile) counter: the sliced kernels' counters each take a 128-byte line of
 // their own (their workgroups read and update them every few steps, and counters sharing a line
@@ -52,13 +56,13 @@ struct PackedLayout {
   size_t bias;   // f32 [L][4][HP]: b_ih + b_hh
   size_t wlin;   // f32 [O][HP]
   size_t blin;   // f32 [O]
-  size_t wrec;   // rec_ok: f16 W_hh fragments of the layer-sequential kernel, [L][8 slices][8 waves][8
-                 // chunks][4 gates][64 lanes][8]
+  size_t wrec;   // rec_ok: f16 W_hh fragments of the layer-sequential kernel, [L][S slices][8 waves][HP / 32
+                 // chunks][NJ tiles][64 lanes][8] (Rec<HP>)
   size_t wih;    // rec_ok: f16 W_ih of every layer the projection GEMM computes, as its W operand:
                  // [4 HP][kp0] (layer 0, unless rec_x0), then [4 HP][kp] per layer >= 1; rows permuted to the
                  // recurrent kernel's lane order, K zero-padded
   size_t wx0;    // rec_ok with rec_x0: f16 MFMA A fragments of W_ih of layer 0 for the recurrent kernel,
-                 // [8 slices][8 waves][2 gates][64 lanes][8] (wave w: unit group w % 4, gates 2 (w / 4) + 0..1)
+                 // [S slices][8 waves][NJ tiles][64 lanes][8] (HP x 128 halfs)
   size_t total;
 };
 PackedLayout packed_layout(const Geometry& g);
@@ -77,14 +81,16 @@ PackedLayout packed_layout(const Geometry& g);
 //   gates    f16 [T * rows][4 HP] fragment-blocked one layer's input projection x_t W_ih^T, columns
 //                                                  in the recurrent kernel's lane order
 //   xs       f16 [2][T * rows][HP] fragment-blocked layer inputs/outputs, alternating (x in slot 0
-//                                                  when layer 0's projection is a GEMM)
+//                                                  when layer 0's projection is a GEMM and kp0 <= HP)
+//   xin      f16 [T * rows][kp0]   fragment-blocked x, when layer 0's projection is a GEMM with
+//                                                  kp0 > HP (input size above the padded H)
 // (fragment-blocked: see blocked_index; one 1 KB block per 16 rows x 32 columns)
 //   xp       f16x8 [ntile][T][4][16]               with rec_x0: x in B-fragment order, K zero-padded
 //                                                  to 32 (layer 0's in-kernel projection)
 // and an xring of one layer, followed by u32 [ntile][8]: the XCD id of each slice (+1), zeroed with
 // the ring before each launch.
 struct WorkspaceLayout {
-  size_t status, counters, xp, hseq, xring, gates, xs, total;
+  size_t status, counters, xp, hseq, xring, gates, xs, xin, total;
   size_t xring_words;  // u64 words of xring (0 unless sliced)
   int chunk_rows;  // batch rows per persistent launch (co-residency bound), multiple of tile_rows
   int tile_rows;   // batch rows per workgroup: 8 or 16
@@ -154,11 +160,11 @@ const void* sliced_kernel(int HP, int wg_tiles);
 int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err);
 hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t s);
 
-// Layer-sequential path (plh_rec.hip): W_hh fragments of one layer, x of a launch's rows into
-// xs slot 0 (blocked [T * rows_pad][HP], zero past the launch's rows and past I up to kp0), and the
-// recurrent kernel of a.layer (x0: with layer 0's in-kernel input projection).
+// Layer-sequential path (plh_rec.hip): W_hh fragments of one layer, x of a launch's rows into the
+// first GEMM's input (blocked [T * rows_pad][ld], zero past the launch's rows and past I up to kp0),
+// and the recurrent kernel of a.layer (x0: with layer 0's in-kernel input projection).
 hipError_t launch_pack_rec_layer(const Geometry& g, int layer, const _Float16* w_hh, _Float16* wpack, hipStream_t s);
-hipError_t launch_rec_input(const Geometry& g, const ForwardArgs& a, _Float16* xs0, hipStream_t s);
+hipError_t launch_rec_input(const Geometry& g, const ForwardArgs& a, _Float16* xs0, int ld, hipStream_t s);
 // W_ih ([4H][K]) of one layer as the projection GEMM's W operand ([4 HP][Kp], lane-ordered rows,
 // zero columns K..Kp-1).
 hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, int Kp, _Float16* dst, hipStream_t s);
@@ -169,9 +175,10 @@ const void* rec_kernel(int HP, bool x0);
 // Time-parallel input projection (plh_gemm.hip): C[m][n] = sum_k X[m][k] W[n][k] for m < M, n < N,
 // fp16 operands and result, fp32 accumulation.  Row-major X [M][ldx], W [N][K], C [M][ldc], or with
 // `blocked` X and C in fragment-blocked order, [M / 16][ld / 32][64 lanes][8] (block (mb, g), lane l:
-// row 16 mb + l % 16, columns 32 g + 8 (l / 16) + 0..7).  K % 128 == 0, K <= 512, N % 128 == 0,
-// ldx >= K and ldc >= N multiples of 8 (blocked: of 32, M % 16 == 0), 16-byte aligned pointers
-// (gemm_shape_ok).  A persistent launch of about one workgroup per CU.
+// row 16 mb + l % 16, columns 32 g + 8 (l / 16) + 0..7).  K % 128 == 0, K <= kGemmMaxKTotal,
+// N % 128 == 0, ldx >= K and ldc >= N multiples of 8 (blocked: of 32, M % 16 == 0), 16-byte aligned
+// pointers (gemm_shape_ok).  A persistent launch of about one workgroup per CU.
+constexpr int kGemmMaxKTotal = 1 << 16;
 bool gemm_shape_ok(long long M, int N, int K, long long ldx, long long ldc, bool blocked);
 hipError_t launch_proj_gemm(const _Float16* X, long long ldx, const _Float16* W, int K, _Float16* C, long long ldc,
                             long long M, int N, bool blocked, int cus, hipStream_t s);

@@ -9,30 +9,30 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
     *why = "input_size, hidden_size and num_layers must be positive and output_size non-negative";
     return false;
   }
-  int HP = 0;
-  if (H <= 32) HP = 32;
-  else if (H <= 64) HP = 64;
-  else if (H <= 128) HP = 128;
-  else if (H <= 256) HP = 256;
-  else if (H <= 512) HP = 512;
-  if (HP == 0) {
-    *why = "hidden_size > 512 is not implemented by the persistent kernels";
+  if (H > kMaxHidden) {
+    *why = "hidden_size > 1024 is not implemented by the persistent kernels";
     return false;
   }
-  if (I > HP) {
-    *why = "input_size larger than the padded hidden size is not implemented";
+  if ((long long)I > (long long)kGemmMaxKTotal) {
+    *why = "input_size > 65536 is not implemented";
     return false;
   }
   if (L > 64 || O > 4096) {
     *why = "num_layers > 64 or output_size > 4096 is not implemented";
     return false;
   }
+  int HP = H <= 32 ? 32 : H <= 64 ? 64 : H <= 128 ? 128 : H <= 256 ? 256 : H <= 512 ? 512 : 1024;
+  // An input wider than the padded hidden size does not fit the all-layers kernels' resident input
+  // part: such a model runs layer by layer (its layer-0 projection a GEMM over any K), whose kernels
+  // start at padded H 128 (the extra padded units stay exactly zero).
+  if (I > HP && HP < 128) HP = 128;
   g->I = I;
   g->H = H;
   g->L = L;
   g->O = O;
   g->HP = HP;
-  g->rec_ok = HP == 512 ? 1 : 0;
+  g->wave_ok = (HP <= 512 && I <= HP) ? 1 : 0;
+  g->rec_ok = (HP >= 512 || I > HP) ? 1 : 0;
   g->rec = 0;
   g->slices = HP == 256 ? Sliced<256>::kS : HP == 512 ? Sliced<512>::kS : 1;
   g->max_wg_tiles = HP == 256 ? 2 : 1;
@@ -40,7 +40,8 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
   g->kci = HP / 32;
   g->kc = 2 * g->kci;
   g->g_in0 = (I + 7) / 8;
-  g->rec_x0 = (g->rec_ok && I <= 32) ? 1 : 0;
+  // Layer 0's projection inside the recurrent kernel: one MFMA K chunk of x (I <= 32), at H 512 / 1024.
+  g->rec_x0 = (g->rec_ok && HP >= 512 && I <= 32) ? 1 : 0;
   g->kp0 = g->rec_x0 ? 0 : (I + 127) / 128 * 128;
   g->kp = (H + 127) / 128 * 128;
   return true;
@@ -49,7 +50,8 @@ bool make_geometry(int I, int H, int L, int O, Geometry* g, std::string* why) {
 Geometry as_layer_sequential(const Geometry& g) {
   Geometry r = g;
   r.rec = 1;
-  r.slices = Rec<512>::kS;
+  r.slices = rec_slices(g.HP);
+  r.waves = 8;
   r.max_wg_tiles = 1;
   if (r.rec_x0) r.g_in0 = 4;  // x as one zero-padded MFMA K chunk
   return r;
@@ -62,8 +64,8 @@ PackedLayout packed_layout(const Geometry& g) {
   size_t off = 0;
   p.wpack = off;
   // HP / 16 gate-row groups x kc chunks of 64 lanes x 8 halfs per gate: the same size whether one
-  // workgroup or `slices` workgroups hold a layer.
-  off = align256(off + (size_t)g.L * (g.HP / 16) * g.kc * 4 * 64 * 8 * sizeof(_Float16));
+  // workgroup or `slices` workgroups hold a layer (the all-layers kernels only).
+  if (g.wave_ok) off = align256(off + (size_t)g.L * (g.HP / 16) * g.kc * 4 * 64 * 8 * sizeof(_Float16));
   p.bias = off;
   off = align256(off + (size_t)g.L * 4 * g.HP * sizeof(float));
   p.wlin = off;
@@ -76,7 +78,7 @@ PackedLayout packed_layout(const Geometry& g) {
   p.wih = off;
   if (g.rec_ok) off = align256(off + (size_t)4 * g.HP * (g.kp0 + (size_t)(g.L - 1) * g.kp) * sizeof(_Float16));
   p.wx0 = off;
-  if (g.rec_ok && g.rec_x0) off = align256(off + (size_t)Rec<512>::kS * 8 * 2 * 64 * 8 * sizeof(_Float16));
+  if (g.rec_ok && g.rec_x0) off = align256(off + (size_t)g.HP * 128 * sizeof(_Float16));
   p.total = off;
   return p;
 }
@@ -93,10 +95,11 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   if (g.rec) {
     // xp (rec_x0 only) holds x as [ntile][T][4][16] f16x8
     w.hseq = w.xring = align256(w.xp + (g.rec_x0 ? ntile * seq_len * 4 * 16 * 16 : 0));
-    w.xring_words = ntile * 2 * g.HP * 8 + ntile * 4;  // the ring, then an 8-entry u32 XCD table per tile
+    w.xring_words = ntile * (2 * g.HP * 8 + 16);  // the ring, then a 32-entry u32 XCD table per tile
     w.gates = align256(w.xring + w.xring_words * sizeof(uint64_t));
     w.xs = align256(w.gates + (size_t)seq_len * chunk_rows * 4 * g.HP * sizeof(_Float16));
-    w.total = align256(w.xs + (size_t)2 * seq_len * chunk_rows * g.HP * sizeof(_Float16));
+    w.xin = align256(w.xs + (size_t)2 * seq_len * chunk_rows * g.HP * sizeof(_Float16));
+    w.total = align256(w.xin + (g.kp0 > g.HP ? (size_t)seq_len * chunk_rows * g.kp0 * sizeof(_Float16) : 0));
     return w;
   }
   w.hseq = align256(w.xp + ntile * seq_len * g.g_in0 * tile_rows * 16);
@@ -104,7 +107,7 @@ WorkspaceLayout workspace_layout(const Geometry& g, int seq_len, int chunk_rows,
   // the rings, then a u32 table of the slices' XCD ids, up to 16 per (layer, tile)
   w.xring_words = g.slices > 1 ? (size_t)g.L * ntile * (2 * g.HP * 8 + 8) : 0;
   w.total = align256(w.xring + w.xring_words * sizeof(uint64_t));
-  w.gates = w.xs = w.total;
+  w.gates = w.xs = w.xin = w.total;
   return w;
 }
 
@@ -117,9 +120,9 @@ static const void* recurrent_kernel(const Geometry& g, int tile_rows, bool ragge
 
 int recurrent_capacity(const Geometry& g, int tile_rows, hipError_t* err) {
   // The smallest occupancy of the variants (with and without lengths, every tile count, with and
-  // without the in-kernel layer-0 projection), so any fits.
+  // without the in-kernel layer-0 projection where it exists), so any fits.
   int cap = 0;
-  for (int v = 0; v < 2 * g.max_wg_tiles * (g.rec ? 2 : 1); ++v) {
+  for (int v = 0; v < 2 * g.max_wg_tiles * (g.rec && g.rec_x0 ? 2 : 1); ++v) {
     const bool ragged = v & 1;
     const bool x0 = g.rec && (v / (2 * g.max_wg_tiles)) == 1;
     const void* fn = recurrent_kernel(g, tile_rows, ragged, 1 + (v / 2) % g.max_wg_tiles, x0);

@@ -1,95 +1,130 @@
-// plh_rec.hip -- the layer-sequential path for padded H = 512 on CDNA4 (gfx950).
+// plh_rec.hip -- the layer-sequential path on CDNA4 (gfx950), padded H 128, 256, 512 and 1024.
 //
 // With [W_ih | W_hh] resident (plh_sliced.hip) a layer of H = 512 needs 16 workgroups per 16-row
-// tile, so a 256-CU device covers 64 rows of all layers per launch.  Here each layer's input
-// projection for all T steps is one GEMM (x_t W_ih^T, fp16 in and out with fp32 accumulation, as
-// the reference's torch::matmul of fp16 tensors; plh_gemm.hip, launched by the host) and the
-// persistent kernel below keeps only W_hh resident: 8 workgroups ("slices") per 16-row tile, 64
-// hidden units each, so one launch covers 512 rows of one layer.  The layers run one after another.
-// Layer 0 with I <= 32 needs no GEMM: its x_t W_ih^T is one K chunk of MFMAs inside the kernel (the
-// X0 variant), from x packed in B-fragment order, so nothing of size T x rows x 4H is written.
+// tile, so a 256-CU device covers 64 rows of all layers per launch, and a layer of H = 1024 would not
+// fit at all.  Here each layer's input projection for all T steps is one GEMM (x_t W_ih^T, fp16 in
+// and out with fp32 accumulation, as the reference's torch::matmul of fp16 tensors; plh_gemm.hip,
+// launched by the host) and the persistent kernel below keeps only W_hh resident: S workgroups
+// ("slices") per 16-row tile, HS hidden units each (the Rec<HP> table of plh_device.h: 8 slices of
+// 64 units at H = 512, 32 slices of 32 units at H = 1024), so one launch covers 512 rows of one
+// layer at H = 512 and 128 rows at H = 1024.  The layers run one after another.  This path also
+// serves input sizes above the padded hidden size (any H), whose layer-0 input part the all-layers
+// kernels cannot hold.  Layer 0 with I <= 32 (H 512, 1024) needs no GEMM: its x_t W_ih^T is one K
+// chunk of MFMAs inside the kernel (the X0 variant), from x packed in B-fragment order, so nothing
+// of size T x rows x 4H is written.
 //   * the GEMM's output columns are in lane order: W_ih's rows are permuted (and padded to 4 HP) at
-//     pack time so that the 8 projections one lane needs per step (4 gates x 2 units) are 16
+//     pack time so that the projections one lane needs per step (4 gates x NJ units) are 8 NJ
 //     contiguous bytes, one load, issued a step ahead; projections and layer inputs are kept
 //     fragment-blocked (1 KB per 16 rows x 32 columns), so a wave's projection load and the
-//     GEMM's stores and loads each move one contiguous 1 KB block;
-//   * wave w of a slice holds the i, f, g, o rows of W_hh for its 8 units (8 w .. 8 w + 7) over all
-//     of K, as two 16-row tiles whose rows interleave the gates (row r: gate r % 4 of unit
-//     4 j + r / 4): 16 K-chunks x 2 tiles of MFMA A fragments (128 VGPRs);
-//   * per step each wave computes its gate sums from h_{t-1} in LDS (32 MFMAs, two independent
-//     chains) and each lane then holds all four gates of units (eu, eu + 4) for one row, so the
-//     cell update needs no other wave: no partial sums and no barrier between a wave's MFMAs and
-//     its gate math, and one wave of a SIMD updates its cells while the other still runs its
-//     MFMAs.  h is double-buffered in LDS by step;
+//     GEMM's stores and loads each move contiguous 1 KB blocks;
+//   * wave w of a slice holds the i, f, g, o rows of W_hh for its 4 NJ units over all of K, as NJ
+//     16-row tiles whose rows interleave the gates (row r: gate r % 4 of unit 4 j + r / 4): KCH
+//     K-chunks x NJ tiles of MFMA A fragments (128 VGPRs at H 512 and 1024);
+//   * per step each wave computes its gate sums from h_{t-1} in LDS (KCH NJ MFMAs in two independent
+//     chains: one per tile, or at NJ = 1 the even and the odd K chunks) and each lane then holds all
+//     four gates of its units for one row, so the cell update needs no other wave: no partial sums
+//     and no barrier between a wave's MFMAs and its gate math, and one wave of a SIMD updates its
+//     cells while the other still runs its MFMAs.  h is double-buffered in LDS by step;
 //   * the slices exchange h_t every step through a two-slot ring of tagged 64-bit words, with the
 //     protocol of plh_sliced.hip (readers re-poll words until their tags are current) but packed
-//     words: 4 fp16 and a 4-bit step tag each, and each workgroup polls only its 7 siblings;
-//     when the 8 slices of a tile run on one XCD (checked at entry) the words stay in its L2
-//     (same_xcd_group: the step's wait for its siblings' words fell from ~2900 to ~1350 cycles);
-//     h_t also goes to the next layer's GEMM input, stored a step later from LDS.
+//     words: 4 fp16 and a 4-bit step tag each, and each workgroup polls only its S - 1 siblings;
+//     when the slices of a tile run on one XCD (checked at entry) the words stay in its L2
+//     (same_xcd_group: the step's wait for its siblings' words fell from ~2900 to ~1350 cycles at
+//     H 512); h_t also goes to the next layer's GEMM input, stored a step later from LDS.
 //
 // Reference behaviour restated (mantuoluozk/persistent_lstm_hip): the generic path's per-layer
-// input projection followed by a persistent recurrence (persistent_lstm_hip.cu:2923-3181), gate
-// order i, f, g, o and the c/h recurrence of persistent_lstm_reference.cpp:21-35.
+// input projection followed by a persistent recurrence (persistent_lstm_hip.cu:2923-3181, which
+// serves 1 <= H <= 1024 and any input size), gate order i, f, g, o and the c/h recurrence of
+// persistent_lstm_reference.cpp:21-35.
+#include <type_traits>
+
 #include "plh_device.h"
 
 namespace plh {
 namespace {
 
-// [L][S][8 waves][16 chunks][2 tiles][64 lanes][8]: wave w of slice s holds the W_hh rows of its 8
-// units s * 64 + 8 w .. + 7 for all of K; row r of tile j's A fragment is gate r % 4 of unit
-// s * 64 + 8 w + 4 j + r / 4, so the D fragment of tile j gives lane l all four gates of unit
-// s * 64 + 8 w + 4 j + l / 16 for batch row l % 16.
+// [L][S][8 waves][KCH chunks][NJ tiles][64 lanes][8]: wave w of slice s holds the W_hh rows of its
+// units s HS + UPW w .. + UPW - 1 for all of K; row r of tile j's A fragment is gate r % 4 of unit
+// s HS + UPW w + 4 j + r / 4, so the D fragment of tile j gives lane l all four gates of unit
+// s HS + UPW w + 4 j + l / 16 for batch row l % 16.
 template <int HP>
 __global__ void pack_rec_kernel(const _Float16* __restrict__ w_hh, int H, _Float16* __restrict__ dst) {
   using C = Rec<HP>;
-  const size_t total = (size_t)C::kS * 8 * C::kKch * 2 * 64 * 8;
+  constexpr int NJ = C::kNj, KCH = C::kKch;
+  const size_t total = (size_t)C::kS * 8 * KCH * NJ * 64 * 8;
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= total) return;
   const int jj = e & 7;
   const int lane = (e >> 3) & 63;
-  const int j = (e >> 9) & 1;
-  const int kc = (int)((e >> 10) % C::kKch);
-  const size_t wsl = (e >> 10) / C::kKch;
-  const int wv = (int)(wsl & 7);
-  const int sl = (int)(wsl >> 3);
+  size_t rest = e >> 9;
+  const int j = (int)(rest % NJ);
+  rest /= NJ;
+  const int kc = (int)(rest % KCH);
+  rest /= KCH;
+  const int wv = (int)(rest & 7);
+  const int sl = (int)(rest >> 3);
   const int r = lane & 15;
-  const int u = sl * C::kHs + wv * 8 + 4 * j + (r >> 2);
+  const int u = sl * C::kHs + wv * C::kUpw + 4 * j + (r >> 2);
   const int q = r & 3;
   const int k = kc * 32 + (lane >> 4) * 8 + jj;
   dst[e] = (u < H && k < H) ? w_hh[((size_t)q * H + u) * H + k] : (_Float16)0.0f;
 }
 
-// W_ih ([4H][K], torch layout) as the GEMM's W operand [4 HP][Kp] with rows in lane order: row
-// ((slice * 8 + wave) * 4 + kgx) * 8 + 2 q + j is gate q of unit slice * 64 + 8 wave + kgx + 4 j, the
-// element 2 q + j that lane kgx * 16 + en of that wave and slice reads from the projection; zero rows
-// for padded units and zero columns K..Kp-1.
+// Lane order of the projection GEMM's output columns (its W operand's rows): column `col` of a
+// [.. x 4 HP] projection holds gate *q of hidden unit *u.
+//   NJ = 2: col = ((slice * 8 + wave) * 4 + kgx) * 8 + 2 q + j for unit slice * 64 + 8 wave + kgx + 4 j:
+//           lane kgx * 16 + en of that wave reads the 8 halfs of its units (eu, eu + 4) as 16 bytes.
+//   NJ = 1: col = ((slice * 4 + wave / 2) * 4 + kgx) * 8 + 4 (wave % 2) + q for unit
+//           slice * 32 + 4 wave + kgx: the two waves of a pair share a 32-column block, lane
+//           kgx * 16 + en of each reading its 4 halfs (8 bytes) of the lane's 16.
+__host__ __device__ inline void rec_lane_column(int col, int HP, int* u, int* q) {
+  if (HP == 1024) {
+    const int wpar = (col >> 2) & 1, kgx = (col >> 3) & 3, pair = (col >> 5) & 3, slice = col >> 7;
+    *q = col & 3;
+    *u = slice * 32 + (pair * 2 + wpar) * 4 + kgx;
+  } else {
+    const int j = col & 1, kgx = (col >> 3) & 3, wave = (col >> 5) & 7, slice = col >> 8;
+    *q = (col & 7) >> 1;
+    *u = slice * 64 + wave * 8 + kgx + 4 * j;
+  }
+}
+
+// W_ih ([4H][K], torch layout) as the GEMM's W operand [4 HP][Kp] with rows in lane order
+// (rec_lane_column); zero rows for padded units and zero columns K..Kp-1.
 __global__ void pack_rec_wih_kernel(const _Float16* __restrict__ w_ih, int H, int HP, int K, int Kp,
                                     _Float16* __restrict__ dst) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (size_t)4 * HP * Kp) return;
   const int col = (int)(e / Kp), k = (int)(e % Kp);
-  const int q = (col & 7) >> 1, j = col & 1, kgx = (col >> 3) & 3, wave = (col >> 5) & 7, slice = col >> 8;
-  const int u = slice * 64 + wave * 8 + kgx + 4 * j;
+  int u, q;
+  rec_lane_column(col, HP, &u, &q);
   dst[e] = (u < H && k < K) ? w_ih[((size_t)q * H + u) * K + k] : (_Float16)0.0f;
 }
 
-// W_ih of layer 0 (I <= 32) as MFMA A fragments of the X0 kernel: [8 slices][8 waves][2 tiles][64 lanes][8],
-// tile j's rows as in pack_rec_kernel (gate r % 4 of unit 8 w + 4 j + r / 4) and k = 8 (l / 16) + 0..7.
+// W_ih of layer 0 (I <= 32) as MFMA A fragments of the X0 kernel: [S][8 waves][NJ tiles][64 lanes][8],
+// tile j's rows as in pack_rec_kernel (gate r % 4 of unit s HS + UPW w + 4 j + r / 4) and
+// k = 8 (l / 16) + 0..7.
+template <int HP>
 __global__ void pack_rec_wx0_kernel(const _Float16* __restrict__ w_ih, int H, int I, _Float16* __restrict__ dst) {
+  using C = Rec<HP>;
+  constexpr int NJ = C::kNj;
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (size_t)Rec<512>::kS * 8 * 2 * 64 * 8) return;
-  const int jj = e & 7, lane = (e >> 3) & 63, j = (e >> 9) & 1, wv = (e >> 10) & 7, sl = (int)(e >> 13);
+  if (e >= (size_t)C::kS * 8 * NJ * 64 * 8) return;
+  const int jj = e & 7, lane = (e >> 3) & 63;
+  size_t rest = e >> 9;
+  const int j = (int)(rest % NJ);
+  rest /= NJ;
+  const int wv = (int)(rest & 7), sl = (int)(rest >> 3);
   const int r = lane & 15;
-  const int u = sl * Rec<512>::kHs + wv * 8 + 4 * j + (r >> 2);
+  const int u = sl * C::kHs + wv * C::kUpw + 4 * j + (r >> 2);
   const int q = r & 3, k = (lane >> 4) * 8 + jj;
   dst[e] = (u < H && k < I) ? w_ih[((size_t)q * H + u) * I + k] : (_Float16)0.0f;
 }
 
-// x rows [row0, row_end) into the first GEMM's input, fragment-blocked [T * rows_pad][HP] (row
+// x rows [row0, row_end) into the first GEMM's input, fragment-blocked [T * rows_pad][LD] (row
 // t * rows_pad + b): columns 0..KP-1, zero past I and past the launch's rows.
 __global__ void rec_input_kernel(const _Float16* __restrict__ x, int T, int I, int row0, int row_end, int rows_pad,
-                                 int HP, int KP, _Float16* __restrict__ xs) {
+                                 int LD, int KP, _Float16* __restrict__ xs) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (size_t)T * rows_pad * KP) return;
   const int i = (int)(e % KP);
@@ -97,16 +132,22 @@ __global__ void rec_input_kernel(const _Float16* __restrict__ x, int T, int I, i
   const int b = (int)(tb % rows_pad);
   const int t = (int)(tb / rows_pad);
   const int r = row0 + b;
-  xs[blocked_index(tb, i, HP)] = (r < row_end && i < I) ? x[((size_t)r * T + t) * I + i] : (_Float16)0.0f;
+  xs[blocked_index(tb, i, LD)] = (r < row_end && i < I) ? x[((size_t)r * T + t) * I + i] : (_Float16)0.0f;
 }
 
 // X0: layer 0 with I <= 32, its input projection computed here from xp (a.gates unused).
 template <int HP, bool X0>
 __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   using C = Rec<HP>;
-  constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch;
-  constexpr int NT = 512, FV = 64, NW = 4;  // packed words each thread gathers per step (at most)
-  constexpr int PW = C::kWords / 2;          // packed words of one step's h of a tile (4 fp16 each)
+  constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch, NJ = C::kNj, UPW = C::kUpw;
+  constexpr int NT = 512, FV = 64;
+  constexpr int PW = C::kWords / 2;      // packed words of one step's h of a tile (4 fp16 each)
+  constexpr int G = (S - 1) * 2 * HS;    // 16-byte loads of the siblings' words per workgroup and step
+  constexpr int NL = (G + NT - 1) / NT;  // loads per thread (at most): 1 at H 128/256, 2 at 512, 4 at 1024
+  constexpr int NW = 2 * NL;             // exchange words a thread gathers per step (at most)
+  // The step input: a lane's projections (NJ = 2: 8 halfs, NJ = 1: 4 halfs), or under X0 x_t as the
+  // lane's MFMA B fragment.
+  using GV = std::conditional_t<(X0 || NJ == 2), f16x8, f16x4>;
 
   // h of all HP units in fragment order, double-buffered by step: step t reads h_{t-1} from buffer
   // t & 1 and writes h_t (its own units and the gathered ones) into the other, so no wave waits for
@@ -123,9 +164,9 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   sliced_coords(blockIdx.x, a.ntile, S, a.xcd_map, unused_layer, tile, slice);
   const int layer = a.layer;
   const int en = lane & 15, kgx = lane >> 4;
-  // This lane's units eu and eu + 4 of row en: the D fragments of the wave's two tiles (all four
-  // gates of unit 8 wave + 4 j + kgx of the slice, row en).
-  const int eu = slice * HS + wave * 8 + kgx;
+  // This lane's units eu + 4 j (j < NJ) of row en: the D fragments of the wave's tiles (all four
+  // gates of unit UPW wave + 4 j + kgx of the slice, row en).
+  const int eu = slice * HS + wave * UPW + kgx;
   const int b = tile * 16 + en;  // row within this launch
   const int grow = a.row0 + b;
   const bool row_ok = grow < a.row_end;
@@ -136,7 +177,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // A failed wait of an earlier layer's launch (this forward's status word) fails this one too,
     // so that the head is poisoned whichever layer timed out.
     s_fail = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-    // With xcd_map the 8 slices of a tile are dispatched to one XCD (workgroups go round-robin over
+    // With xcd_map the S slices of a tile are dispatched to one XCD (workgroups go round-robin over
     // the XCDs, and theirs are congruent mod 8); checked here, and only then do they exchange h
     // through that XCD's L2 (same_xcd_group; the table follows the ring).
     s_l2 = 0;
@@ -160,21 +201,21 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // readfirstlane, so that the loop's exits are uniform branches the compiler leaves unstructured.
   const int Tt = __builtin_amdgcn_readfirstlane(s_tlen);
 
-  f16x8 w[KCH][2];
+  f16x8 w[KCH][NJ];
   {
     const f16x8* wp =
-        reinterpret_cast<const f16x8*>(a.wpack) + (size_t)((layer * S + slice) * 8 + wave) * KCH * 2 * 64 + lane;
+        reinterpret_cast<const f16x8*>(a.wpack) + (size_t)((layer * S + slice) * 8 + wave) * KCH * NJ * 64 + lane;
 #pragma unroll
     for (int kc = 0; kc < KCH; ++kc)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) w[kc][j] = wp[(kc * 2 + j) * 64];
+      for (int j = 0; j < NJ; ++j) w[kc][j] = wp[(kc * NJ + j) * 64];
   }
-  // X0: W_ih of layer 0 for the wave's two tiles.
-  f16x8 wx[2] = {};
+  // X0: W_ih of layer 0 for the wave's tiles.
+  f16x8 wx[NJ] = {};
   if constexpr (X0) {
-    const f16x8* p = reinterpret_cast<const f16x8*>(a.wx0) + (size_t)(slice * 8 + wave) * 2 * 64 + lane;
-    wx[0] = p[0];
-    wx[1] = p[64];
+    const f16x8* p = reinterpret_cast<const f16x8*>(a.wx0) + (size_t)(slice * 8 + wave) * NJ * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) wx[j] = p[j * 64];
   }
   // The resident weights complete here (otherwise the compiler keeps them "possibly outstanding"
   // and waits for every global access in flight before the step loop's MFMAs).
@@ -184,10 +225,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     s_bias[q][u] = a.bias[((size_t)layer * 4 + q) * HP + slice * HS + u];
   }
 
-  float c[2];
-  _Float16 hcur[2];
+  float c[NJ];
+  _Float16 hcur[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int u = eu + 4 * j;
     const bool v = row_ok && u < a.H;
     const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
@@ -209,50 +250,68 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   }
   __syncthreads();  // hbuf and s_bias complete before the first step (or the head, if no step runs)
 
-  // Input projection of step min(t, Tt - 1) for this lane's row and units, bias excluded: element
-  // 2 q + j is gate q of unit eu + 4 j.  Padded units read zero columns and padded rows zero inputs.
-  // One unconditional 16-byte load (a load under an exec branch makes the compiler wait for it
-  // together with the ring poll), consumed a step after it is issued.
+  // Input projection of step min(t, Tt - 1) for this lane's row and units, bias excluded: gate q of
+  // unit eu + 4 j is element 2 q + j (NJ = 2) or q (NJ = 1).  Padded units read zero columns and
+  // padded rows zero inputs.  One unconditional load (a load under an exec branch makes the compiler
+  // wait for it together with the ring poll), consumed a step after it is issued.
   // X0: instead, x of step min(t, Tt - 1) as this lane's MFMA B fragment (row en, k 8 kgx .. +7) from
   // xp ([ntile][T][4][16] f16x8).
-  // Blocked projections: step t's 16 rows of this tile are block row t * ntile + tile; this lane's
-  // 16 bytes are lane kgx * 16 + en of column block slice * 8 + wave (32 columns per block).
-  const f16x8* gsrc = X0 ? nullptr
-                         : reinterpret_cast<const f16x8*>(a.gates) + ((size_t)tile * (4 * HP / 32) + slice * 8 + wave) * 64 +
-                               kgx * 16 + en;
-  const f16x8* xsrc = X0 ? a.xp + (size_t)tile * a.T * 64 + kgx * 16 + en : nullptr;
-  auto gload = [&](int t) -> f16x8 {
+  // Blocked projections: step t's 16 rows of this tile are block row t * ntile + tile of 4 HP / 32
+  // column blocks; this lane's bytes are those of lane kgx * 16 + en of its wave's column block
+  // (rec_lane_column).
+  constexpr size_t kColBlocks = 4 * HP / 32;
+  const GV* gsrc = nullptr;
+  size_t gstride = 0;
+  if constexpr (X0) {
+    gsrc = a.xp + (size_t)tile * a.T * 64 + kgx * 16 + en;
+    gstride = 64;
+  } else if constexpr (NJ == 2) {
+    gsrc = reinterpret_cast<const f16x8*>(a.gates) + ((size_t)tile * kColBlocks + slice * 8 + wave) * 64 + kgx * 16 + en;
+    gstride = (size_t)a.ntile * kColBlocks * 64;
+  } else {
+    gsrc = reinterpret_cast<const f16x4*>(a.gates) +
+           (((size_t)tile * kColBlocks + slice * 4 + (wave >> 1)) * 64 + kgx * 16 + en) * 2 + (wave & 1);
+    gstride = (size_t)a.ntile * kColBlocks * 64 * 2;
+  }
+  auto gload = [&](int t) -> GV {
     const size_t tc = (size_t)(t < Tt ? t : Tt - 1);
-    if constexpr (X0) return xsrc[tc * 64];
-    return gsrc[tc * a.ntile * (4 * HP / 32) * 64];
+    return gsrc[tc * gstride];
   };
 
-  // Packed exchange (xw_* words): a word carries units eu, eu + 1 (low half) and eu + 4, eu + 5 (high
-  // half) of one row from a lane with even kgx, which holds eu and eu + 4 and takes eu + 1 and eu + 5
-  // from its partner lane + 16.  Words are in writer order [slice][wave][row en][kgx / 2]: the two
-  // words of a 16-byte load are units 8 w .. 8 w + 7 of one row, one f16x8 of h's fragment order.
+  // Packed exchange (xw_* words): a word carries 4 units of one row.  NJ = 2: units eu, eu + 1 (low
+  // half) and eu + 4, eu + 5 (high half) from a lane with even kgx, which holds eu and eu + 4 and
+  // takes eu + 1 and eu + 5 from its partner lane + 16; words in writer order
+  // [slice][wave][row en][kgx / 2].  NJ = 1: units 4 w .. 4 w + 3 of the wave from lane kgx = 0,
+  // which takes unit +1 from lane + 16 and the pair +2, +3 from lane + 32; words in writer order
+  // [slice][wave / 2][row en][wave % 2].  Either way the two words of a 16-byte load are units
+  // 8 m .. 8 m + 7 of one row, one f16x8 of h's fragment order.
   uint64_t* ring = a.xring + (size_t)tile * 2 * C::kWords;  // a slot of PW words per step parity
-  const int pwoff = (slice * 8 + wave) * 32 + en * 2 + (kgx >> 1);  // this lane's word (even kgx)
-  // A workgroup gathers the 7 sibling slices' words (its own pairs go to hbuf from registers): load
-  // k of a thread reads words 2 (tid % 128) and 2 (tid % 128) + 1 of sibling block 4 k + tid / 128
-  // (the blocks in slice order without this workgroup's own), so waves 0-5 issue 2 loads, 6-7 one.
-  const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7);
-  const int nld = quarter < 3 ? 2 : 1;
+  const int pwoff = NJ == 2 ? (slice * 8 + wave) * 32 + en * 2 + (kgx >> 1)
+                            : ((slice * 4 + (wave >> 1)) * 16 + en) * 2 + (wave & 1);  // this lane's word
+  const bool writer = NJ == 2 ? (kgx & 1) == 0 : kgx == 0;
+  // A workgroup gathers the S - 1 sibling slices' words (its own pairs go to hbuf from registers):
+  // load k of thread tid is load index g = 512 k + tid of the step, 2 HS loads per sibling block
+  // (the blocks in slice order without this workgroup's own); g < G.  Block and validity are
+  // wave-uniform (2 HS and G are multiples of 64).
+  const int wbase = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
+  const int nld = wbase < G ? ((G - wbase + NT - 1) / NT < NL ? (G - wbase + NT - 1) / NT : NL) : 0;
+  const int q_in = (int)threadIdx.x % (2 * HS);  // load position within a sibling block
   auto sib = [&](int k) {
-    const int r = 4 * k + quarter;
+    const int r = (k * NT + wbase) / (2 * HS);
     return r + (r >= slice ? 1 : 0);
   };
-  // hbuf position (f16x8 index) of load k of this thread: units 8 (tid % 128 / 16) .. + 7 of the
-  // sibling's block, row tid % 16, i.e. (sib * HS / 8 + tid % 128 / 16) * 16 + tid % 16; a wave's
-  // loads fill 64 consecutive f16x8 (1 KB), so its one 16-byte LDS store per load is conflict-free.
-  auto gdst16 = [&](int k) -> int { return sib(k) * (HS / 8) * 16 + (int)(threadIdx.x & 127); };
-  const int own_dst = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);  // this lane's word's first pair in hbuf (even kgx)
+  // hbuf position (f16x8 index) of load k: sibling block sib * 2 HS + q, i.e. units 8 (q / 16) .. + 7
+  // of the sibling's block, row q % 16; a wave's loads fill 64 consecutive f16x8 (1 KB), so its one
+  // 16-byte LDS store per load is conflict-free.
+  auto gdst16 = [&](int k) -> int { return sib(k) * 2 * HS + q_in; };
+  // this lane's word's first pair in hbuf (writer lanes): u32 index of units eu, eu + 1
+  const int own_dst = ((eu >> 3) * 16 + en) * 4 + ((eu & 7) >> 1);
   // b_ih + b_hh of this lane's units (eu + 4 j) by gate, in registers for the whole sequence.
-  float bias[4][2];
+  float bias[4][NJ];
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) bias[q][j] = s_bias[q][wave * 8 + kgx + 4 * j];
+    for (int j = 0; j < NJ; ++j) bias[q][j] = s_bias[q][wave * UPW + kgx + 4 * j];
 
   int probe_i = 0;
   // Probe steps live in SGPRs (a VGPR loaded in the loop would put a vmcnt(0) on every step).
@@ -260,7 +319,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   auto write_probe = [&](int pi) {
     if (!row_ok) return;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int u = eu + 4 * j;
       if (u < a.H) {
         const size_t o = (((size_t)pi * a.L + layer) * a.B + grow) * a.H + u;
@@ -270,10 +329,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     }
   };
 
-  uint64_t wv[NW] = {};  // poll results (words of waves with one load: the first two)
-  // The next layer's input: h_t of this slice's 64 units x 16 rows, written a step later from
-  // hbuf in 16-byte pieces, fragment-blocked: two contiguous 1 KB blocks (row block t * ntile + tile,
-  // column blocks 2 slice and 2 slice + 1), one per wave.
+  uint64_t wv[NW] = {};  // poll results
+  // The next layer's input: h_t of this slice's HS units x 16 rows, written a step later from
+  // hbuf in 16-byte pieces, fragment-blocked (row block t * ntile + tile, column blocks of the
+  // slice's units), by the first 2 HS threads.
   constexpr int kCopyThreads = HS * 16 / 8;
   const int copy_row = threadIdx.x & 15, copy_k8 = slice * (HS / 8) + (threadIdx.x >> 4) % (HS / 8);
   const int copy_src = copy_k8 * 16 + copy_row;  // f16x8 index of (row, units 8 copy_k8 ..) in hbuf
@@ -286,26 +345,33 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // Step t + 1's projection is loaded first: it retires before this step's ring poll (loads retire
   // in order), about 2000 cycles later, so only stores are in flight when a step ends, on every
   // path (loop exits included), and the gate math never waits for a load.
-  auto step = [&](int t, f16x8& gp) -> bool {
-    f16x8 gn = gload(t + 1);
+  auto step = [&](int t, GV& gp) -> bool {
+    GV gn = gload(t + 1);
     const f16x8* const hprev = hbuf[t & 1];
     f16x8* const hnext = hbuf[(t + 1) & 1];
-    // The gate sums of the wave's two tiles over all of K (X0: plus x_t W_ih^T), two independent
-    // MFMA chains fed by one 16-byte LDS read per K chunk.
+    // The gate sums over all of K (X0: plus x_t W_ih^T) in two independent MFMA chains fed by one
+    // 16-byte LDS read per K chunk: one chain per tile (NJ = 2), or the even and the odd K chunks of
+    // the one tile (NJ = 1, summed before the gate math).
     // The accumulators start at bias + x_t W_ih^T (X0: at the bias), added here, where the second
     // wave of a SIMD waits for the matrix core anyway, rather than between the MFMAs and the gate math.
     f32x4 acc[2];
+    if constexpr (NJ == 2) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[j][q] = X0 ? bias[q][j] : bias[q][j] + (float)gp[2 * q + j];
+        for (int q = 0; q < 4; ++q) acc[j][q] = X0 ? bias[q][j] : bias[q][j] + (float)gp[2 * q + j];
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[0][q] = X0 ? bias[q][0] : bias[q][0] + (float)gp[q];
+      acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     if constexpr (X0) {
-      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[0], gp, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[1], gp, acc[1], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wx[j], gp, acc[j], 0, 0, 0);
     }
     // The h fragments are read from LDS four K-chunks ahead of their MFMAs (one read in flight
     // per chunk would leave the matrix core waiting for LDS latency at every chunk).
-    constexpr int kAhead = 4;
+    constexpr int kAhead = KCH < 4 ? KCH : 4;
     f16x8 bq[kAhead];
 #pragma unroll
     for (int i = 0; i < kAhead; ++i) bq[i] = hprev[i * FV + lane];
@@ -313,31 +379,40 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     for (int kc = 0; kc < KCH; ++kc) {
       const f16x8 bv = bq[kc % kAhead];
       if (kc + kAhead < KCH) bq[kc % kAhead] = hprev[(kc + kAhead) * FV + lane];
-      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][0], bv, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][1], bv, acc[1], 0, 0, 0);
+      if constexpr (NJ == 2) {
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][0], bv, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][1], bv, acc[1], 0, 0, 0);
+      } else {
+        acc[kc & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][0], bv, acc[kc & 1], 0, 0, 0);
+      }
     }
-    // h_{t-1} of this slice's units, 16 bytes per thread of waves 0-1, stored below as the next
-    // layer's input (hbuf[t & 1] is overwritten only in step t + 1).
+    // h_{t-1} of this slice's units, 16 bytes per thread of the first 2 HS threads, stored below as
+    // the next layer's input (hbuf[t & 1] is overwritten only in step t + 1).
     f16x8 hcp = {};
     if (!last && threadIdx.x < kCopyThreads) hcp = hprev[copy_src];
 
-    // Gate math on the accumulators: element q of tile j is gate q of unit eu + 4 j.
+    // Gate math on the accumulators: gate q of unit eu + 4 j.
     const bool live = t < len;
     {
-      float z[4][2];
+      float z[4][NJ];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          z[q][j] = acc[j][q];
-      float cn[2] = {c[0], c[1]}, hn[2];
+        for (int j = 0; j < NJ; ++j) z[q][j] = NJ == 2 ? acc[j][q] : acc[0][q] + acc[1][q];
+      float cn[NJ], hn[NJ];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn[j], hn[j]);
+      for (int j = 0; j < NJ; ++j) {
+        cn[j] = c[j];
+        lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn[j], hn[j]);
+      }
       // Both units' updates are computed on every lane and then selected: otherwise the compiler
       // puts each behind a branch on `live`, which serialises the two units' dependency chains.
-      asm volatile("" : "+v"(cn[0]), "+v"(cn[1]), "+v"(hn[0]), "+v"(hn[1]));
+      if constexpr (NJ == 2)
+        asm volatile("" : "+v"(cn[0]), "+v"(cn[1]), "+v"(hn[0]), "+v"(hn[1]));
+      else
+        asm volatile("" : "+v"(cn[0]), "+v"(hn[0]));
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         c[j] = live ? cn[j] : c[j];
         hcur[j] = live ? (_Float16)hn[j] : hcur[j];
       }
@@ -353,17 +428,22 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // This step's ring slot, uniform by construction: the compiler would otherwise keep its address
     // in VGPRs (it flows through the lane-conditional store) and put every poll in a waterfall loop.
     uint64_t* const slot = ring + (size_t)__builtin_amdgcn_readfirstlane(t & 1) * PW;
-    // The word's pairs (eu, eu + 1) and (eu + 4, eu + 5): this lane holds eu and eu + 4, its
-    // partner lane + 16 (kgx + 1) eu + 1 and eu + 5.
+    // The word's two pairs: NJ = 2: (eu, eu + 1) and (eu + 4, eu + 5), this lane holding eu and
+    // eu + 4, its partner lane + 16 (kgx + 1) eu + 1 and eu + 5.  NJ = 1: (eu, eu + 1) from this lane
+    // and lane + 16, (eu + 2, eu + 3) from lanes + 32 and + 48 (the pair lane + 32 assembled).
     uint32_t pair_lo, pair_hi;
     {
-      const uint32_t mine = xw_enc_pair((uint32_t)__builtin_bit_cast(uint16_t, hcur[0]) |
-                                        ((uint32_t)__builtin_bit_cast(uint16_t, hcur[1]) << 16));
+      uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, hcur[0]);
+      if constexpr (NJ == 2) bits |= (uint32_t)__builtin_bit_cast(uint16_t, hcur[1]) << 16;
+      const uint32_t mine = xw_enc_pair(bits);
       const uint32_t other = (uint32_t)__builtin_amdgcn_ds_swizzle((int)mine, 0x401F);  // lane ^ 16
       pair_lo = __builtin_amdgcn_perm(other, mine, 0x05040100u);
-      pair_hi = __builtin_amdgcn_perm(other, mine, 0x07060302u);
+      if constexpr (NJ == 2)
+        pair_hi = __builtin_amdgcn_perm(other, mine, 0x07060302u);
+      else
+        pair_hi = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 32) & 63) << 2, (int)pair_lo);
       const uint64_t word = ((uint64_t)pair_lo | ((uint64_t)pair_hi << 32)) | want_bits;
-      if ((kgx & 1) == 0) {
+      if (writer) {
         if (l2)
           __hip_atomic_store(slot + pwoff, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         else
@@ -378,10 +458,9 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // load, so it is read whole; its own tag validates it (the two words of a load may come from
     // different steps, and a load is repeated until both are current).  Half the load
     // instructions of 8-byte atomic loads: C4 21.5 -> 20.0 ms.
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(slot, 0, PW * 8, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(slot, 0, PW * 8, 0x00020000);
     auto pload = [&](int p) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (threadIdx.x & 127) * 16u, sib(p) * (PW / 8) * 8, 16);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (unsigned)q_in * 16u, sib(p) * HS * 32, 16);
       wv[2 * p] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
       wv[2 * p + 1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
     };
@@ -398,21 +477,21 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     else
       __builtin_amdgcn_s_sleep(6);
 #pragma unroll
-    for (int p = 0; p < NW / 2; ++p)
+    for (int p = 0; p < NL; ++p)
       if (p < nld) pload(p);
     // This slice's own pairs of h_t, from the lanes that send them (nobody reads hbuf[(t + 1) & 1]
     // in step t).
-    if ((kgx & 1) == 0) {
+    if (writer) {
       uint32_t* own32 = reinterpret_cast<uint32_t*>(hnext);
       own32[own_dst] = xw_dec_pair(pair_lo);
-      own32[own_dst + 2] = xw_dec_pair(pair_hi);
+      own32[own_dst + (NJ == 2 ? 2 : 1)] = xw_dec_pair(pair_hi);
     }
     if (!last) {
       if (threadIdx.x < kCopyThreads && t > 0) copy_out(t - 1, hcp);
     } else if (a.out_seq && row_ok) {
       _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NJ; ++j)
         if (eu + 4 * j < a.H) dst[4 * j] = live ? hcur[j] : (_Float16)0.0f;
     }
     if (t + 1 == probe_next) {
@@ -443,7 +522,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       }
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
-      for (int p = 0; p < NW / 2; ++p)
+      for (int p = 0; p < NL; ++p)
         if (p < nld && !(xw_tag_is(wv[2 * p], want_bits) & xw_tag_is(wv[2 * p + 1], want_bits))) pload(p);
     }
     // gn's load was issued before this step's poll, so it has completed (loads retire in order);
@@ -459,19 +538,21 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     asm volatile("" : "+v"(gn));
     gp = gn;
 #pragma unroll
-    for (int k = 0; k < NW / 2; ++k)
+    for (int k = 0; k < NL; ++k)
       if (k < nld) {
-        // words 2 k (units +0, +1 | +4, +5) and 2 k + 1 (+2, +3 | +6, +7) of one row
+        // NJ = 2: words 2 k (units +0, +1 | +4, +5) and 2 k + 1 (+2, +3 | +6, +7) of one row;
+        // NJ = 1: words 2 k (units +0, +1 | +2, +3) and 2 k + 1 (+4, +5 | +6, +7).
         typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-        const u32x4 v = {xw_dec_pair((uint32_t)wv[2 * k]), xw_dec_pair((uint32_t)wv[2 * k + 1]),
-                         xw_dec_pair((uint32_t)(wv[2 * k] >> 32)), xw_dec_pair((uint32_t)(wv[2 * k + 1] >> 32))};
+        const uint32_t a0 = xw_dec_pair((uint32_t)wv[2 * k]), a1 = xw_dec_pair((uint32_t)(wv[2 * k] >> 32));
+        const uint32_t b0 = xw_dec_pair((uint32_t)wv[2 * k + 1]), b1 = xw_dec_pair((uint32_t)(wv[2 * k + 1] >> 32));
+        const u32x4 v = NJ == 2 ? u32x4{a0, b0, a1, b1} : u32x4{a0, a1, b0, b1};
         hnext[gdst16(k)] = __builtin_bit_cast(f16x8, v);
       }
     lds_barrier();
     return __builtin_amdgcn_readfirstlane(s_fail) == 0;
   };
 
-  f16x8 gp = {};
+  GV gp = {};
   if (Tt > 0) gp = gload(0);
   // Nothing in flight at the loop entry, so the first gate math waits for no load.
   wait_vmem_all();
@@ -501,7 +582,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   if (!ok) {
     // A wait failed, here or in an earlier layer's launch (the status word records it): poison every
     // output of this workgroup (states, probes, output sequence, head) and leave.
-    if (row_ok) poison_lane_outputs(a, layer, grow, eu, 2, last, 4);
+    if (row_ok) poison_lane_outputs(a, layer, grow, eu, NJ, last, 4);
     if (last && slice == 0 && a.out) {
       for (int idx = threadIdx.x; idx < 16 * a.O; idx += NT) {
         const int gr = a.row0 + tile * 16 + idx / a.O;
@@ -516,7 +597,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     for (int t = Tt; t < a.T; ++t) {
       _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NJ; ++j)
         if (eu + 4 * j < a.H) dst[4 * j] = (_Float16)0.0f;
     }
   }
@@ -527,7 +608,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   }
   if (row_ok) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int u = eu + 4 * j;
       if (u < a.H) {
         const size_t si = ((size_t)layer * a.B + grow) * a.H + u;
@@ -560,14 +641,31 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
 
 inline unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
 
+template <int HP>
+hipError_t pack_rec_layer_hp(int H, const _Float16* w_hh, _Float16* dst, hipStream_t s) {
+  const size_t n = (size_t)4 * HP * HP;
+  hipLaunchKernelGGL(pack_rec_kernel<HP>, blocks_for(n, 256), 256, 0, s, w_hh, H, dst);
+  return hipGetLastError();
+}
+
+template <int HP>
+hipError_t pack_rec_wx0_hp(int H, int I, const _Float16* w_ih0, _Float16* dst, hipStream_t s) {
+  const size_t n = (size_t)HP * 128;
+  hipLaunchKernelGGL(pack_rec_wx0_kernel<HP>, blocks_for(n, 256), 256, 0, s, w_ih0, H, I, dst);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_pack_rec_layer(const Geometry& g, int layer, const _Float16* w_hh, _Float16* wpack, hipStream_t s) {
-  if (g.HP != 512) return hipErrorInvalidValue;
-  using C = Rec<512>;
-  const size_t per_layer = (size_t)C::kS * 8 * C::kKch * 2 * 64 * 8;
-  hipLaunchKernelGGL(pack_rec_kernel<512>, blocks_for(per_layer, 256), 256, 0, s, w_hh, g.H, wpack + layer * per_layer);
-  return hipGetLastError();
+  _Float16* dst = wpack + (size_t)layer * 4 * g.HP * g.HP;
+  switch (g.HP) {
+    case 128: return pack_rec_layer_hp<128>(g.H, w_hh, dst, s);
+    case 256: return pack_rec_layer_hp<256>(g.H, w_hh, dst, s);
+    case 512: return pack_rec_layer_hp<512>(g.H, w_hh, dst, s);
+    case 1024: return pack_rec_layer_hp<1024>(g.H, w_hh, dst, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, int Kp, _Float16* dst, hipStream_t s) {
@@ -577,24 +675,34 @@ hipError_t launch_pack_rec_wih(const Geometry& g, const _Float16* w_ih, int K, i
 }
 
 hipError_t launch_pack_rec_wx0(const Geometry& g, const _Float16* w_ih0, _Float16* dst, hipStream_t s) {
-  if (g.HP != 512 || g.I > 32) return hipErrorInvalidValue;
-  const size_t n = (size_t)Rec<512>::kS * 8 * 2 * 64 * 8;
-  hipLaunchKernelGGL(pack_rec_wx0_kernel, blocks_for(n, 256), 256, 0, s, w_ih0, g.H, g.I, dst);
-  return hipGetLastError();
+  if (g.I > 32) return hipErrorInvalidValue;
+  switch (g.HP) {
+    case 512: return pack_rec_wx0_hp<512>(g.H, g.I, w_ih0, dst, s);
+    case 1024: return pack_rec_wx0_hp<1024>(g.H, g.I, w_ih0, dst, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
-hipError_t launch_rec_input(const Geometry& g, const ForwardArgs& a, _Float16* xs0, hipStream_t s) {
+hipError_t launch_rec_input(const Geometry& g, const ForwardArgs& a, _Float16* xs0, int ld, hipStream_t s) {
   const size_t n = (size_t)a.T * a.rows_pad * g.kp0;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(rec_input_kernel, blocks_for(n, 256), 256, 0, s, a.x, a.T, g.I, a.row0, a.row_end, a.rows_pad,
-                     g.HP, g.kp0, xs0);
+                     ld, g.kp0, xs0);
   return hipGetLastError();
 }
 
 const void* rec_kernel(int HP, bool x0) {
-  if (HP != 512) return nullptr;
-  return x0 ? reinterpret_cast<const void*>(&lstm_rec_kernel<512, true>)
-            : reinterpret_cast<const void*>(&lstm_rec_kernel<512, false>);
+  switch (HP) {
+    case 128: return x0 ? nullptr : reinterpret_cast<const void*>(&lstm_rec_kernel<128, false>);
+    case 256: return x0 ? nullptr : reinterpret_cast<const void*>(&lstm_rec_kernel<256, false>);
+    case 512:
+      return x0 ? reinterpret_cast<const void*>(&lstm_rec_kernel<512, true>)
+                : reinterpret_cast<const void*>(&lstm_rec_kernel<512, false>);
+    case 1024:
+      return x0 ? reinterpret_cast<const void*>(&lstm_rec_kernel<1024, true>)
+                : reinterpret_cast<const void*>(&lstm_rec_kernel<1024, false>);
+    default: return nullptr;
+  }
 }
 
 }  // namespace plh

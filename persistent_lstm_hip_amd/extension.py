@@ -366,7 +366,7 @@ class NativeLibrary:
         Row-major (blocked=False): x [rows, K] fp16 with unit column stride (its row stride may exceed
         K), out [rows, cols].  Fragment-blocked (blocked=True): x is a contiguous [rows, ldx] tensor
         in the layout of `to_blocked` (the first K columns are used), out likewise [rows, cols]
-        blocked.  w: [cols, K] fp16; K % 128 == 0, K <= 512, cols % 128 == 0.  Replaces the
+        blocked.  w: [cols, K] fp16; K % 128 == 0, K <= 65536, cols % 128 == 0.  Replaces the
         reference's torch::matmul input projection (persistent_lstm_hip.cu:2988-2994).  Launched on
         the current stream."""
         for name, t in (("x", x), ("w", w)):

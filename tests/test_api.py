@@ -66,9 +66,16 @@ def test_unsupported_structures_fall_back_to_native(kwargs, name):
 
 
 def test_unsupported_size_falls_back_to_native():
-    conv = P.convert_regressor_module(make_regressor(5, 520, 1, 4))
+    # the reference's generic path serves H <= 1024 (model.py:163); beyond that the module stays native
+    conv = P.convert_regressor_module(make_regressor(5, 1100, 1, 4))
     assert isinstance(conv, P.NativeModuleFallback)
     assert conv.backend_name == "native_pytorch_unsupported_geometry"
+
+
+@pytest.mark.parametrize("I,H", [(5, 520), (5, 1024), (300, 256), (70, 50)])
+def test_wide_sizes_convert_to_the_hip_module(I, H):
+    conv = P.convert_regressor_module(make_regressor(I, H, 1, 4))
+    assert isinstance(conv, P.PersistentLSTMRegressor), (I, H)
 
 
 def test_convert_rejects_non_regressors():

@@ -49,38 +49,49 @@ def test_abi_version_and_error_text(ext):
     assert ext.lib.plh_abi_version() == 1
     assert ext.lib.plh_supports(5, 4096, 4, 24) == 0
     assert "hidden_size" in ext.last_error()
+    assert ext.lib.plh_supports(5, 1024, 4, 24) == 1 and ext.lib.plh_supports(300, 256, 2, 6) == 1
 
 
 @pytest.mark.parametrize("I,H,L,O,ok", [
     (5, 128, 4, 24, True), (5, 1, 1, 1, True), (32, 32, 2, 0, True), (64, 64, 8, 3, True), (128, 128, 1, 24, True),
     (5, 129, 4, 24, True), (5, 256, 4, 24, True), (5, 512, 4, 24, True), (300, 300, 2, 1, True),
-    (5, 513, 4, 24, False), (33, 32, 2, 4, False), (257, 256, 2, 4, False), (0, 128, 4, 24, False), (5, 128, 0, 24, False), (5, 128, 4, -1, False),
+    # the reference's generic entry point serves 1 <= H <= 1024 and any input size
+    # (model.py:154-165, persistent_lstm_hip.cu:2981-2991): H 513..1024 and I > padded H run layer by layer
+    (5, 513, 4, 24, True), (5, 1024, 4, 24, True), (300, 256, 2, 6, True), (33, 32, 2, 4, True),
+    (257, 256, 2, 4, True), (1000, 600, 1, 3, True), (4096, 1024, 2, 1, True),
+    (5, 1025, 4, 24, False), (70000, 128, 1, 1, False), (0, 128, 4, 24, False), (5, 128, 0, 24, False),
+    (5, 128, 4, -1, False),
 ])
 def test_supported_geometries(ext, I, H, L, O, ok):
     assert ext.supports(I, H, L, O) is ok
 
 
 def test_packed_bytes_closed_form(ext):
-    # wpack: L * (HP/16 waves) * (2*HP/32 chunks) * 4 gates * 64 lanes * 16 B, then f32 bias, head, all 256-aligned
+    # wpack (the all-layers kernels, HP <= 512 and I <= HP): L * (HP/16 waves) * (2*HP/32 chunks) * 4 gates
+    # * 64 lanes * 16 B; then f32 bias, head; all 256-aligned.  The layer-sequential path (HP >= 512, or
+    # I > HP with HP raised to 128 at least) adds its W_hh fragments (4HP x HP fp16 per layer), W_ih of every
+    # layer its projection GEMM computes ([4HP][K padded to 128]: layer 0 only when I > 32 or HP < 512)
+    # and, when layer 0's projection runs in its recurrent kernel (HP >= 512, I <= 32), layer 0's W_ih as
+    # MFMA fragments (HP x 128 fp16).
     a = lambda v: (v + 255) // 256 * 256  # noqa: E731
     r128 = lambda v: (v + 127) // 128 * 128  # noqa: E731
     for I, H, L, O, HP in [(5, 128, 4, 24, 128), (5, 100, 2, 3, 128), (5, 40, 3, 7, 64), (5, 10, 1, 0, 32),
                            (5, 256, 4, 24, 256), (5, 200, 2, 3, 256), (5, 512, 4, 24, 512), (7, 400, 1, 1, 512),
-                           (40, 300, 3, 2, 512)]:
+                           (40, 300, 3, 2, 512), (5, 1024, 4, 24, 1024), (5, 600, 2, 3, 1024), (300, 1000, 2, 1, 1024),
+                           (300, 256, 2, 6, 256), (33, 32, 2, 4, 128), (1000, 600, 1, 3, 1024), (200, 130, 3, 2, 256)]:
+        wave_ok = HP <= 512 and I <= HP
+        rec_ok = HP >= 512 or I > HP
+        x0 = rec_ok and HP >= 512 and I <= 32
         wp = L * (HP // 16) * (HP // 16) * 4 * 64 * 16
-        want = a(wp) + a(L * 4 * HP * 4) + a(O * HP * 4) + a(O * 4)
-        if HP == 512:
-            # both paths' operands: the layer-sequential kernel's W_hh fragments (half of the above);
-            # W_ih of every layer its projection GEMM computes, [4HP][K padded to 128] - layer 0 only when
-            # I > 32, else layer 0's W_ih as the recurrent kernel's MFMA fragments (8 slices x 8 waves x
-            # 2 gates x 64 lanes x 16 B)
-            kp0 = 0 if I <= 32 else r128(I)
-            want += a(wp // 2) + a(4 * HP * (kp0 + (L - 1) * r128(H)) * 2)
-            if I <= 32:
-                want += a(8 * 8 * 2 * 64 * 16)
-        assert ext.packed_bytes(I, H, L, O) == want
+        want = (a(wp) if wave_ok else 0) + a(L * 4 * HP * 4) + a(O * HP * 4) + a(O * 4)
+        if rec_ok:
+            kp0 = 0 if x0 else r128(I)
+            want += a(L * 4 * HP * HP * 2) + a(4 * HP * (kp0 + (L - 1) * r128(H)) * 2)
+            if x0:
+                want += a(HP * 128 * 2)
+        assert ext.packed_bytes(I, H, L, O) == want, (I, H, L, O)
     with pytest.raises(ValueError):
-        ext.packed_bytes(5, 1000, 4, 24)
+        ext.packed_bytes(5, 1025, 4, 24)
 
 
 def test_workspace_bytes_grow_with_sequence(ext):
@@ -127,7 +138,7 @@ def test_layer_sequential_workspace_layout(ext):
     b = ext.workspace_bytes(5, H, L, 24, 512, T)
     gates = T * rows * 4 * H * 2
     xs = 2 * T * rows * H * 2
-    ring = (rows // 16) * (2 * H * 8 * 8 + 8 * 4)  # + the tile's table of its 8 slices' XCD ids
+    ring = (rows // 16) * (2 * H * 8 * 8 + 16 * 8)  # + the tile's table of up to 32 slices' XCD ids
     xp = rows * T * 64
     assert gates + xs + ring + xp <= b < gates + xs + ring + xp + (1 << 12)
     # I > 32: layer 0's projection is a GEMM too (x goes to the first xs buffer): no packed x
@@ -143,11 +154,37 @@ def test_layer_sequential_workspace_layout(ext):
     assert wave <= b < wave + (1 << 12)
 
 
+def test_wide_hidden_and_input_workspace_layout(ext):
+    # H 513..1024 (padded 1024): only the layer-sequential path; 32 slices of 32 units per 16-row tile,
+    # so 256 / 32 = 8 tiles (128 rows) per launch.  I <= 32: x packed for layer 0's in-kernel projection.
+    L, T, H = 2, 100, 1024
+    rows = 128
+    gates = T * rows * 4 * H * 2
+    xs = 2 * T * rows * H * 2
+    ring = (rows // 16) * (2 * H * 8 * 8 + 16 * 8)
+    xp = rows * T * 64
+    b = ext.workspace_bytes(5, 700, L, 3, 512, T)
+    assert gates + xs + ring + xp <= b < gates + xs + ring + xp + (1 << 12)
+    # an input wider than the padded H gets its own GEMM input buffer [T * rows][K padded to 128]
+    b = ext.workspace_bytes(1100, 700, L, 3, 512, T)
+    xin = T * rows * 1152 * 2
+    assert gates + xs + ring + xin <= b < gates + xs + ring + xin + (1 << 12)
+    # I = 300 > H = 256: layer by layer at padded H 256 (4 slices of 64 units per tile, so 64 tiles = 1024
+    # rows per launch); x fits the first layer-input buffer (K padded to 384 > 256: its own buffer)
+    rows, H = 512, 256
+    b = ext.workspace_bytes(300, H, L, 6, 512, T)
+    gates = T * rows * 4 * H * 2
+    xs = 2 * T * rows * H * 2
+    ring = (rows // 16) * (2 * H * 8 * 8 + 16 * 8)
+    xin = T * rows * 384 * 2
+    assert gates + xs + ring + xin <= b < gates + xs + ring + xin + (1 << 12)
+
+
 def test_forward_validates_before_touching_the_device(ext):
     f = ext.lib.plh_forward
     ws = ctypes.c_void_p(256)  # never dereferenced: validation fails first
     # unsupported geometry
-    assert f(ws, 5, 999, 4, 24, ws, 4, 4, None, None, None, None, None, None, None, None, 0, None, None, ws, 1 << 20,
+    assert f(ws, 5, 1999, 4, 24, ws, 4, 4, None, None, None, None, None, None, None, None, 0, None, None, ws, 1 << 20,
              None) == PLH_ERR_UNSUPPORTED
     # missing packed weights
     assert f(None, 5, 128, 4, 24, ws, 4, 4, None, None, None, None, None, None, None, None, 0, None, None, ws, 1 << 20,

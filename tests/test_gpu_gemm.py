@@ -27,6 +27,9 @@ def _check(got: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str) -> No
     (257, 128, 128, 64),      # smallest N; x rows wider than K (ldx > K)
     (5, 384, 1024, 128),      # fewer rows than one tile; K = 300 padded to 384 in a 512-wide buffer
     (70000, 256, 384, 0),     # m-groups with several tiles each at a width of three slices
+    (3000, 640, 512, 0),      # K > 512: W held in K blocks of 512 and 128, reloaded per m-tile
+    (1100, 1024, 4096, 0),    # the H 1024 layer shape: two K blocks of 512
+    (600, 2048, 256, 128),    # four K blocks, x rows wider than K
 ])
 def test_input_projection_matches_float64(gpu, M, K, N, pad):
     print(f"[gpu-case] input projection M={M} K={K} N={N} pad={pad}", flush=True)
@@ -43,6 +46,7 @@ def test_input_projection_matches_float64(gpu, M, K, N, pad):
     (512000, 512, 2048, 512),  # the C4 layer shape in the layer-sequential path's layout
     (4000, 128, 512, 128),     # the C2 layer shape
     (1616, 384, 2048, 512),    # H = 300 padded to 384 within a 512-wide layer buffer; 101 row blocks
+    (128000, 1024, 4096, 1024),  # the H 1024 layer shape of one 128-row launch, T = 1000 (two K blocks)
 ])
 def test_input_projection_blocked_layout(gpu, M, K, N, ldx):
     """Fragment-blocked x and out (the layout the layer-sequential path keeps): the result equals the
@@ -81,6 +85,6 @@ def test_input_projection_output_stride_and_repeat(gpu):
 def test_input_projection_rejects_bad_shapes(gpu):
     def z(*shape):
         return torch.zeros(*shape, dtype=torch.float16, device="cuda")
-    for xs, ws in (((10, 96), (256, 96)), ((10, 128), (200, 128)), ((10, 640), (256, 640))):
+    for xs, ws in (((10, 96), (256, 96)), ((10, 128), (200, 128)), ((10, 650), (256, 650))):
         with pytest.raises(ValueError, match="k % 128"):
             gpu.input_projection(z(*xs), z(*ws))

@@ -283,6 +283,86 @@ def test_large_hidden_c3_c4(gpu, H):
             _say(f"H={H} {name}@{step}: max_abs={mx:.3e} mean_abs={mn:.3e}")
 
 
+@pytest.mark.parametrize("I,H,L,O,B,T,ragged,state", [
+    (5, 600, 2, 3, 20, 30, False, False),     # padded H 1024, layer 0 projected inside the kernel
+    (5, 1024, 2, 24, 150, 12, True, True),    # H 1024, two launches of 128 + 22 rows, ragged, h0/c0
+    (300, 256, 2, 6, 33, 20, False, True),    # I > H: layer by layer at padded H 256, GEMM K 384
+    (300, 1024, 2, 5, 16, 15, True, False),   # H 1024 with a GEMM-projected layer 0 (K 384)
+    (1000, 600, 1, 3, 18, 12, False, False),  # I 1000: GEMM K 1024 (two K blocks), x in its own buffer
+    (600, 700, 2, 7, 24, 10, False, True),    # K 640: a K block of 512 and one of 128
+    (70, 50, 3, 4, 30, 25, True, False),      # H 50 < I 70: padded to 128, layer by layer
+    (33, 32, 2, 4, 17, 21, False, False),     # H 32 < I 33
+    (40, 520, 1, 2, 300, 6, False, False),    # H 520, three launches of 128 rows
+])
+def test_wide_hidden_and_input_against_oracle(gpu, I, H, L, O, B, T, ragged, state):
+    """The reference's generic entry point serves 1 <= H <= 1024 and any input size
+    (model.py:154-165, persistent_lstm_hip.cu:2981-2991).  Here H 513..1024 and inputs wider than the
+    padded hidden size run the layer-sequential path (projection GEMM + W_hh-only persistent kernel);
+    every output (head, sequence, final h/c, probed h/c) against the C oracle at the north-star
+    tolerance, and the path's own rounding (ref_fp16_proj, or ref_fp16_proj_l1 where layer 0 is
+    projected in the kernel) within the regression bounds."""
+    _say(f"wide I={I} H={H} L={L} O={O} B={B} T={T} ragged={ragged} state={state}")
+    assert gpu.supports(I, H, L, O)
+    torch.manual_seed(1000 + H + I)
+    lstm = torch.nn.LSTM(I, H, L, batch_first=True)
+    head = torch.nn.Linear(H, O)
+    x = torch.randn(B, T, I, generator=torch.Generator().manual_seed(H))
+    g = torch.Generator().manual_seed(I)
+    lengths = torch.randint(0, T + 1, (B,), generator=g) if ragged else None
+    h0 = (0.5 * torch.randn(L, B, H, generator=g)).half() if state else None
+    c0 = (0.5 * torch.randn(L, B, H, generator=g)).half() if state else None
+    probes = [1, max(1, T // 2), T]
+    params = [[getattr(lstm, f"{n}_l{l}").detach().cuda() for l in range(L)]
+              for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+    packed = gpu.pack(*params, head.weight.detach().cuda(), head.bias.detach().cuda())
+    dev = torch.device("cuda")
+    res = gpu.forward(packed, (I, H, L, O), x.to(dev, torch.float16), lengths=lengths,
+                      h0=None if h0 is None else h0.to(dev), c0=None if c0 is None else c0.to(dev),
+                      want_seq=True, want_state=True, probe_steps=probes, check_status=True)
+    kw = dict(lengths=None if lengths is None else lengths.numpy(), h0=None if h0 is None else h0.float().numpy(),
+              c0=None if c0 is None else c0.float().numpy(), probe_steps=probes, want_seq=True)
+    want = oracle.lstm_forward(x.numpy(), oracle_layers(lstm), **kw)
+    tag = f"I={I} H={H}"
+    for k in ("out_seq", "h_n", "c_n", "probe_h", "probe_c"):
+        mx, mn = assert_close(res[k].float().cpu().numpy(), want[k], what=f"{tag} {k}")
+    w_head = oracle.linear(want["h_n"][-1], *linear_params(head))
+    mx, mn = assert_close(res["out"].float().cpu().numpy(), w_head, what=f"{tag} head")
+    _say(f"{tag}: head max_abs {mx:.2e} mean_abs {mn:.2e}")
+    # (every case here runs layer by layer: padded H 1024, or an input above the padded H; layer 0 is
+    # projected inside the kernel, in fp32, when I <= 32)
+    numerics = "ref_fp16_proj_l1" if (I <= 32 and H > 512) else "ref_fp16_proj"
+    ref = oracle.lstm_forward(x.numpy(), oracle_layers(lstm), numerics=numerics, **kw)
+    # a flipped fp16 rounding of a large input projection (I up to 1000) moves a gate by up to half an
+    # fp16 ulp of it: the bound is 20x below the north star's
+    for k, bound in (("probe_h", 1e-3), ("probe_c", 1e-3)):
+        assert_close(res[k].float().cpu().numpy(), ref[k], max_abs=bound, mean_abs=bound / 10,
+                     what=f"{tag} {k} vs {numerics}")
+
+
+def test_generic_projected_entry_point_at_h1024(gpu):
+    """persistent_lstm_hip_ext.persistent_lstm_regressor_forward_generic_projected (bindings.cpp:163) at
+    H = 1024 with the reference's argument formats (torch-layout W_ih/W_hh lists, fp16 fused biases),
+    against the oracle fed the same fp16 values."""
+    import persistent_lstm_hip_ext as ext_mod
+
+    I, H, L, O, B, T = 5, 1024, 2, 24, 40, 20
+    _say("generic_projected H=1024")
+    native = make_regressor(I, H, L, O).half()
+    dev = torch.device("cuda")
+    w_ih = [getattr(native.lstm, f"weight_ih_l{l}").detach().to(dev) for l in range(L)]
+    w_hh = [getattr(native.lstm, f"weight_hh_l{l}").detach().to(dev) for l in range(L)]
+    fused = [(getattr(native.lstm, f"bias_ih_l{l}") + getattr(native.lstm, f"bias_hh_l{l}")).detach().to(dev)
+             for l in range(L)]
+    lw, lb = native.linear.weight.detach().to(dev), native.linear.bias.detach().to(dev)
+    x = make_x(B, T, I).half()
+    got = ext_mod.persistent_lstm_regressor_forward_generic_projected(x.to(dev), w_ih, w_hh, fused, lw, lb)
+    layers = [(w_ih[l].float().cpu().numpy(), w_hh[l].float().cpu().numpy(), fused[l].float().cpu().numpy(), None)
+              for l in range(L)]
+    want = oracle.regressor_forward(x.float().numpy(), layers, lw.float().cpu().numpy(), lb.float().cpu().numpy())
+    mx, mn = assert_close(got.float().cpu().numpy(), want, what="generic_projected H=1024")
+    _say(f"generic_projected H=1024: max_abs {mx:.2e} mean_abs {mn:.2e}")
+
+
 def test_h512_row_pinned_on_both_paths(gpu):
     """At padded H 512 the batch size picks the path (L = 4: B <= 256 the all-layers sliced kernel,
     whose projections stay fp32; B > 256 the layer-sequential path, whose GEMM projections of layers
@@ -597,23 +677,24 @@ def test_mfma_rate_probe(gpu):
 
 
 def test_random_geometry_sweep(gpu):
-    """Seeded random geometries through plh_forward: input size, hidden size (both kernel families,
-    padded and unpadded), layers, head size (0 = no head), batch, length, ragged lengths with zeros,
-    initial states and two probe steps.  Every output (head, sequence, final h/c, probed h/c) is
-    checked against the C oracle at the north-star tolerance."""
-    rng = np.random.default_rng(20261202)
+    """Seeded random geometries through plh_forward: input size (also above the padded hidden size),
+    hidden size 1..1024 (every kernel family, padded and unpadded), layers, head size (0 = no head),
+    batch (above one 128-row launch at padded H 1024), length, ragged lengths with zeros, initial
+    states and two probe steps.  Every output (head, sequence, final h/c, probed h/c) is checked
+    against the C oracle at the north-star tolerance."""
+    rng = np.random.default_rng(20261203)
     device = torch.device("cuda")
     done = 0
-    while done < 48:
-        I = int(rng.integers(1, 41))
-        H = int(rng.integers(1, 129)) if rng.random() < 0.5 else int(rng.integers(129, 513))
+    while done < 64:
+        I = int(rng.integers(1, 41)) if rng.random() < 0.8 else int(rng.integers(41, 700))
+        u = rng.random()
+        H = int(rng.integers(1, 129)) if u < 0.4 else int(rng.integers(129, 513)) if u < 0.75 else \
+            int(rng.integers(513, 1025))
         L = int(rng.integers(1, 5))
         O = 0 if rng.random() < 0.2 else int(rng.integers(1, 31))
-        B = int(rng.integers(1, 71))
+        B = int(rng.integers(1, 71)) if H <= 512 else int(rng.integers(1, 161))
         T = int(rng.integers(1, 121))
-        if I > (32 if H <= 32 else 64 if H <= 64 else 128 if H <= 128 else 256 if H <= 256 else 512):
-            continue  # input_size above the padded hidden size is outside the supported geometries
-        if B * T * L * 4 * H * (I + H) > 3e8:
+        if B * T * L * 4 * H * (I + H) > 4e8:
             continue  # keep the oracle to a fraction of a second per case
         ragged = rng.random() < 0.5
         with_state = rng.random() < 0.5

@@ -260,22 +260,23 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // column blocks; this lane's bytes are those of lane kgx * 16 + en of its wave's column block
   // (rec_lane_column).
   constexpr size_t kColBlocks = 4 * HP / 32;
-  const GV* gsrc = nullptr;
-  size_t gstride = 0;
-  if constexpr (X0) {
-    gsrc = a.xp + (size_t)tile * a.T * 64 + kgx * 16 + en;
-    gstride = 64;
-  } else if constexpr (NJ == 2) {
-    gsrc = reinterpret_cast<const f16x8*>(a.gates) + ((size_t)tile * kColBlocks + slice * 8 + wave) * 64 + kgx * 16 + en;
-    gstride = (size_t)a.ntile * kColBlocks * 64;
-  } else {
-    gsrc = reinterpret_cast<const f16x4*>(a.gates) +
-           (((size_t)tile * kColBlocks + slice * 4 + (wave >> 1)) * 64 + kgx * 16 + en) * 2 + (wave & 1);
-    gstride = (size_t)a.ntile * kColBlocks * 64 * 2;
-  }
+  const f16x8* const xsrc = X0 ? a.xp + (size_t)tile * a.T * 64 + kgx * 16 + en : nullptr;
+  const f16x8* const gsrc8 =
+      (X0 || NJ != 2) ? nullptr
+                      : reinterpret_cast<const f16x8*>(a.gates) + ((size_t)tile * kColBlocks + slice * 8 + wave) * 64 +
+                            kgx * 16 + en;
+  const f16x4* const gsrc4 =
+      (X0 || NJ != 1) ? nullptr
+                      : reinterpret_cast<const f16x4*>(a.gates) +
+                            (((size_t)tile * kColBlocks + slice * 4 + (wave >> 1)) * 64 + kgx * 16 + en) * 2 + (wave & 1);
   auto gload = [&](int t) -> GV {
     const size_t tc = (size_t)(t < Tt ? t : Tt - 1);
-    return gsrc[tc * gstride];
+    if constexpr (X0)
+      return xsrc[tc * 64];
+    else if constexpr (NJ == 2)
+      return gsrc8[tc * a.ntile * kColBlocks * 64];
+    else
+      return gsrc4[tc * a.ntile * kColBlocks * 128];
   };
 
   // Packed exchange (xw_* words): a word carries 4 units of one row.  NJ = 2: units eu, eu + 1 (low
@@ -293,8 +294,12 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   // load k of thread tid is load index g = 512 k + tid of the step, 2 HS loads per sibling block
   // (the blocks in slice order without this workgroup's own); g < G.  Block and validity are
   // wave-uniform (2 HS and G are multiples of 64).
+  // Every thread makes the first G / NT loads; load G / NT exists for the waves below G % NT (a
+  // compile-time count and one wave-uniform flag, so the unconditional loads carry no branch).
+  constexpr int NLF = G / NT;
   const int wbase = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
-  const int nld = wbase < G ? ((G - wbase + NT - 1) / NT < NL ? (G - wbase + NT - 1) / NT : NL) : 0;
+  const bool last_ld = wbase < G - NLF * NT;
+  auto has_ld = [&](int k) { return k < NLF || (k == NLF && last_ld); };
   const int q_in = (int)threadIdx.x % (2 * HS);  // load position within a sibling block
   auto sib = [&](int k) {
     const int r = (k * NT + wbase) / (2 * HS);
@@ -478,7 +483,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       __builtin_amdgcn_s_sleep(6);
 #pragma unroll
     for (int p = 0; p < NL; ++p)
-      if (p < nld) pload(p);
+      if (has_ld(p)) pload(p);
     // This slice's own pairs of h_t, from the lanes that send them (nobody reads hbuf[(t + 1) & 1]
     // in step t).
     if (writer) {
@@ -505,7 +510,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     for (int spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int r = 0; r < NW; ++r) ready = ready & ((r >> 1) >= nld || xw_tag_is(wv[r], want_bits));
+      for (int r = 0; r < NW; ++r) ready = ready & (!has_ld(r >> 1) || xw_tag_is(wv[r], want_bits));
       if (ready) break;
       if (spin == 0) {
         t0 = __builtin_amdgcn_s_memrealtime();
@@ -523,7 +528,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       asm volatile("" ::: "memory");  // the re-polls are not loop-invariant loads
 #pragma unroll
       for (int p = 0; p < NL; ++p)
-        if (p < nld && !(xw_tag_is(wv[2 * p], want_bits) & xw_tag_is(wv[2 * p + 1], want_bits))) pload(p);
+        if (has_ld(p) && !(xw_tag_is(wv[2 * p], want_bits) & xw_tag_is(wv[2 * p + 1], want_bits))) pload(p);
     }
     // gn's load was issued before this step's poll, so it has completed (loads retire in order);
     // the empty asm tells the compiler, which would otherwise count the copy below as a read of a
@@ -539,7 +544,7 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     gp = gn;
 #pragma unroll
     for (int k = 0; k < NL; ++k)
-      if (k < nld) {
+      if (has_ld(k)) {
         // NJ = 2: words 2 k (units +0, +1 | +4, +5) and 2 k + 1 (+2, +3 | +6, +7) of one row;
         // NJ = 1: words 2 k (units +0, +1 | +2, +3) and 2 k + 1 (+4, +5 | +6, +7).
         typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

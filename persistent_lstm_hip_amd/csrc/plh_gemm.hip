@@ -26,6 +26,7 @@
 //   * XCD-aware placement: workgroups are dispatched round-robin over the 8 XCDs (workgroup b on
 //     XCD b % 8), and the n-slices of one m-group share an XCD, so each m-tile of X is read from
 //     HBM about once into that XCD's L2 and then from L2 by the other slices;
+//   * the result goes out with nontemporal stores (it is read back by another kernel, long after);
 //   * two layouts of X and C: row-major ([M][ldx], [M][ldc]), or fragment-blocked: X as
 //     [M / 16][ldx / 32][64 lanes][8] (block (mb, kc) holds rows 16 mb + l % 16, k = 32 kc + 8 (l / 16)
 //     + 0..7 in lane l) and C as [M / 16][ldc / 32][64][8] (n = 32 g + 8 (l / 16) + 0..7).  A lane's
@@ -178,11 +179,16 @@ proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* 
           v[j] = (_Float16)acc[a][2 * p][j];
           v[4 + j] = (_Float16)acc[a][2 * p + 1][j];
         }
+        // Nontemporal stores: the result streams to HBM without displacing the L2-resident X tiles the
+        // other n-slices of the m-group still read (and is consumed by another kernel much later):
+        // [512000,128]x[128,512] 0.148 -> 0.111 ms (4.4 -> 5.9 TB/s), [512000,512]x[512,2048]
+        // 1.06 -> 1.03 ms, interleaved runs on one box.
         if (m < M) {
           if constexpr (BLK)
-            reinterpret_cast<f16x8*>(C)[((size_t)(m >> 4) * (ldc / 32) + (n0 >> 5) + p) * 64 + lane] = v;
+            __builtin_nontemporal_store(
+                v, reinterpret_cast<f16x8*>(C) + ((size_t)(m >> 4) * (ldc / 32) + (n0 >> 5) + p) * 64 + lane);
           else
-            *reinterpret_cast<f16x8*>(C + (size_t)m * ldc + ncol + 32 * p) = v;
+            __builtin_nontemporal_store(v, reinterpret_cast<f16x8*>(C + (size_t)m * ldc + ncol + 32 * p));
         }
       }
     }

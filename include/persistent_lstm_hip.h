@@ -161,7 +161,9 @@ int plh_status(const void* workspace, uint32_t* status, void* stream);
  * plh_kernel_timing(n) with n > 0 arms n pairs of HIP events for the calling thread: each later
  * plh_forward on this thread records one pair around its persistent launch(es) (on the
  * layer-sequential H512 path: around all its projection GEMMs and launches), until the n pairs
- * are used.  plh_kernel_timing(0) disarms.  plh_kernel_timing_read synchronises on the recorded
+ * are used.  plh_kernel_timing(0) disarms.  Called again with the n it was armed with, it re-arms
+ * the same events without creating any (no HIP call: a caller can arm before its warm-ups and
+ * re-arm right before its timed forwards).  plh_kernel_timing_read synchronises on the recorded
  * events and returns the summed elapsed milliseconds and the number of timed forwards.
  * No counterpart in the reference (it only timed whole forwards from Python, LSTM-hip.py:80-91).
  */

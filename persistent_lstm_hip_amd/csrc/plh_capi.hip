@@ -478,8 +478,15 @@ int plh_noalloc_status(uint32_t* status, void* stream) {
 
 int plh_kernel_timing(int max_forwards) {
   KernelTiming& tm = timing();
+  if (max_forwards < 0) {
+    tm.release();
+    return fail(PLH_ERR_INVALID, "max_forwards must be non-negative");
+  }
+  if (max_forwards > 0 && (int)tm.ev.size() == 2 * max_forwards) {
+    tm.used = 0;  // the same count again: re-arm the events already made (no HIP call)
+    return PLH_OK;
+  }
   tm.release();
-  if (max_forwards < 0) return fail(PLH_ERR_INVALID, "max_forwards must be non-negative");
   for (int i = 0; i < 2 * max_forwards; ++i) {
     hipEvent_t e;
     hipError_t err = hipEventCreate(&e);

@@ -676,6 +676,31 @@ def test_mfma_rate_probe(gpu):
     assert 1000.0 < tflops < 3000.0, tflops
 
 
+def test_kernel_timing_rearm(gpu):
+    """plh_kernel_timing: n pairs armed record the next n forwards' persistent launches and no more;
+    arming again with the same n re-arms the same events (the warm-up forwards' records are
+    discarded), and the times are of the order of the forward's own."""
+    _say("kernel timing re-arm")
+    native = make_regressor(5, 64, 2, 3)
+    model = _gpu_model(native)
+    x = make_x(16, 50, 5).to("cuda", torch.float16)
+    with torch.inference_mode():
+        gpu.kernel_timing(3)
+        for _ in range(2):
+            model(x)
+        gpu.kernel_timing(3)  # re-arm: the two forwards above no longer count
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(5):
+            model(x)
+        b.record()
+        torch.cuda.synchronize()
+        ms, n = gpu.kernel_timing_read()
+        gpu.kernel_timing(0)
+    assert n == 3, n
+    assert 0.0 < ms < a.elapsed_time(b), (ms, a.elapsed_time(b))
+
+
 def test_random_geometry_sweep(gpu):
     """Seeded random geometries through plh_forward: input size (also above the padded hidden size),
     hidden size 1..1024 (every kernel family, padded and unpadded), layers, head size (0 = no head),

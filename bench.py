@@ -7,10 +7,9 @@
 Workload (configs[1] of BASELINE.json, "C2"): 4-layer LSTM, input 5, hidden 128, Linear 128 -> 24,
 batch 512, seq 1000, fp16 weights/activations with fp32 accumulation, x ~ N(0, 1), PyTorch-default
 init from torch.manual_seed(42), h0 = c0 = 0.  A "step" is one full forward of that batch; inputs
-are resident in HBM before the timed region.  Timing: `--warmup` untimed forwards (default 50), then
-`--steps` timed forwards (default 100, as the reference's LSTM-hip.py:80-91) between two HIP events.
-The GPU measurements beside the headline (below) run before it, so its warm-ups start on a GPU past
-the clock ramp of a process's first ~30 recurrent-kernel launches, as in a serving process.
+are resident in HBM before the timed region.  Timing: `--warmup` untimed forwards (default 50: the
+GPU's clock ramps up over a process's first ~30 launches of a recurrent kernel), then `--steps`
+timed forwards (default 100, as the reference's LSTM-hip.py:80-91) between two HIP events.
 
 Printed: one JSON line with the driver's fields plus
   roofline         -- the persistent kernel's algorithmic FLOPs per launch / its average duration
@@ -187,12 +186,11 @@ def _kpairs(w: torch.Tensor) -> torch.Tensor:
     return wt.reshape(-1, 2, w.shape[0]).permute(0, 2, 1).contiguous()
 
 
-def dropin_route_timing(native, x, warmup: int, steps: int):
+def dropin_route_timing(native, x, warmup: int, steps: int, module_ms: float) -> dict:
     """The reference dispatcher's per-forward call (model.py:584-656 calls
     persistent_lstm_hip_ext.persistent_lstm4_forward_interleaved with kpairs-packed fp16 weights and
     fp16 fused biases, model.py:548-578) served by this build's drop-in extension module: the same
-    protocol as the headline (warm-ups, then `steps` back-to-back calls between two events).  Only
-    enqueued here (no host synchronisation at its end); the returned function reads the result."""
+    protocol as the headline (warm-ups, then `steps` back-to-back calls between two events)."""
     import persistent_lstm_hip_ext
 
     lstm = native.lstm
@@ -215,14 +213,12 @@ def dropin_route_timing(native, x, warmup: int, steps: int):
         for _ in range(steps):
             out = fwd(x, *args)
         b.record()
-
-    def result() -> dict:
-        b.synchronize()
-        return {"entry_point": "persistent_lstm_hip_ext.persistent_lstm4_forward_interleaved (kpairs weights, "
-                               "fp16 fused bias: the reference dispatcher's default C2 call)",
-                "ms_per_fwd": a.elapsed_time(b) / steps, "steps": steps, "warmup": warmup,
-                "out_checksum": float(out.float().abs().sum())}
-    return result
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    return {"entry_point": "persistent_lstm_hip_ext.persistent_lstm4_forward_interleaved (kpairs weights, fp16 "
+                           "fused bias: the reference dispatcher's default C2 call)",
+            "ms_per_fwd": ms, "vs_module_ms_per_step": ms / module_ms, "steps": steps, "warmup": warmup,
+            "out_checksum": float(out.float().abs().sum())}
 
 
 def uniform_batch_protocol(model, dev, warmup: int, steps: int) -> dict:
@@ -325,21 +321,8 @@ def main() -> int:
     x = x_cpu.to("cuda", torch.float16)
     dev = x.device
 
-    # The measurements beside the headline run first: the projection GEMM, the MFMA peak probe (the
-    # dense fp16 rate this GPU sustains with the kernels' instruction, and the shader clock
-    # meanwhile), the other configurations, the reference's uniform-batch protocol and, last, the
-    # drop-in route, whose forwards are the same C2 forward and are followed by the headline's
-    # warm-ups without a host synchronisation in between.  The GPU's clock falls within a few
-    # forwards of any idle gap (even one of a millisecond) and takes ~40 forwards to climb back, so
-    # this order times the headline near the steady state of a serving process.
-    projection = input_projection_timing(ext, dev)
-    probe_tflops, probe_ghz = ext.probe_mfma_f16()
-    others = other_configs(dev) if not args.no_other_configs else None
-    uniform = uniform_batch_protocol(model, dev, args.warmup, args.steps)
     t_all0, t_all1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ext.kernel_timing(args.steps)  # the events made here; re-armed (no HIP call) after the warm-ups
-    dropin_result = dropin_route_timing(native, x, args.warmup, args.steps)
-
+    ext.kernel_timing(args.steps)  # the events made here, re-armed (no HIP call) after the warm-ups
     with torch.inference_mode():
         for _ in range(args.warmup):
             model(x)
@@ -366,12 +349,17 @@ def main() -> int:
             model(x)
             evs[i][1].record()
         torch.cuda.synchronize()
+    # On-box check of the roofline constant (after the timed region): the dense fp16 MFMA rate this
+    # GPU sustains with the kernels' instruction, and the shader clock meanwhile.
+    dropin = dropin_route_timing(native, x, args.warmup, args.steps, t_all0.elapsed_time(t_all1) / args.steps)
+    probe_tflops, probe_ghz = ext.probe_mfma_f16()
+    projection = input_projection_timing(ext, dev)
+    uniform = uniform_batch_protocol(model, dev, args.warmup, args.steps)
+    others = other_configs(dev) if not args.no_other_configs else None
     total_ms = t_all0.elapsed_time(t_all1)
     per_fwd = sorted(a.elapsed_time(b) for a, b in evs)
     median_ms = statistics.median(per_fwd)
     ms_per_step = total_ms / args.steps
-    dropin = dropin_result()
-    dropin["vs_module_ms_per_step"] = dropin["ms_per_fwd"] / ms_per_step
     kernel_ms = kernel_ms_total / max(n_timed, 1)
     flops = algorithmic_flops(I, H, L, O, B, T)
     achieved = flops / (kernel_ms * 1e-3) / 1e12

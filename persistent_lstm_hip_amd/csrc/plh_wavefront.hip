@@ -201,30 +201,23 @@ __device__ __forceinline__ void wavefront_body(const ForwardArgs& a, WavefrontLd
       if (p / (KCI * FV) < ns_k && p % (KCI * FV) < per) rb[p] = R[i];
     }
   };
-  // Hand-off copy of chunk k's h history (LDS) to the global sequence buffer, in 8-byte words so
-  // that each wave's agent-scope (sc1) store covers one contiguous 512-byte run: sc1 stores are
-  // written through, and two interleaved 8-byte halves of 16-byte elements would each cost a full
-  // line write.  They become visible to other CUs and XCDs once complete, with no L2 write-back.
+  // Hand-off copy of chunk k's h history (LDS) to the global sequence buffer: one 16-byte sc1 buffer
+  // store per thread and element, so a wave's store instruction writes one contiguous 1 KB run (sc1
+  // stores are written through; they become visible to other CUs and XCDs once complete, with no L2
+  // write-back).  The descriptor's size is the chunk's valid bytes: the stores of a partial chunk's
+  // idle lanes fall outside it and are dropped.
   auto copy_out = [&](int k) {
-    const int nw = min(CH, Tt - k * CH) * (KCR * FV) * 2;
-    const uint64_t* hb = reinterpret_cast<const uint64_t*>(hist + (k & 1) * kHistBuf);
-    uint64_t* dst = reinterpret_cast<uint64_t*>(out_seq_h + (size_t)k * CH * hstep);
-    uint64_t v[2 * RN];
-    if (ROWS == 8 && nw == 2 * RN * NT) {  // a full chunk: every thread copies 2 RN words
+    const int nv = min(CH, Tt - k * CH) * (KCR * FV);  // valid f16x8 of the chunk
+    const f16x8* hb = hist + (k & 1) * kHistBuf;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(out_seq_h + (size_t)k * CH * hstep, 0, nv * 16, 0x00020000);
+    f16x8 v[RN];
 #pragma unroll
-      for (int i = 0; i < 2 * RN; ++i) v[i] = hb[(int)threadIdx.x + i * NT];
+    for (int i = 0; i < RN; ++i) v[i] = hb[min((int)threadIdx.x + i * NT, kHistBuf - 1)];
 #pragma unroll
-      for (int i = 0; i < 2 * RN; ++i)
-        __hip_atomic_store(dst + threadIdx.x + i * NT, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * RN; ++i) v[i] = hb[min((int)threadIdx.x + i * NT, nw - 1)];
-#pragma unroll
-    for (int i = 0; i < 2 * RN; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      if (idx < nw) __hip_atomic_store(dst + idx, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (int i = 0; i < RN; ++i)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v[i]),
+                                             rs, (uint32_t)((int)threadIdx.x + i * NT) * 16u, 0, 16);
   };
   auto need_for = [&](int k) -> uint32_t { return (uint32_t)min((k + 1) * CH, Tt); };  // chunk k published
 

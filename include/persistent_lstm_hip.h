@@ -92,7 +92,10 @@ int64_t plh_workspace_bytes(int input_size, int hidden_size, int num_layers, int
  *             probe_h / probe_c device fp32 [n_probe, L, batch, H] receive every layer's state
  *             after that many steps (h as rounded to fp16, c in fp32).  n_probe = 0: no probes.
  *   workspace device memory of at least plh_workspace_bytes(...) bytes, 256-byte aligned.
- * Any output pointer may be NULL.  Asynchronous on `stream`.  Hidden sizes 513..1024, inputs wider
+ * Any output pointer may be NULL.  Asynchronous on `stream`; forwards on different streams of one
+ * device are ordered by the library (each needs the whole device co-resident): the first forward
+ * on a second stream synchronises the device once, later ones wait on an event of the previous
+ * forward when it was on another stream (not inside a stream capture).  Hidden sizes 513..1024, inputs wider
  * than the padded hidden size, and at padded H 512 a batch that needs more wavefront launches than
  * there are layers run layer by layer: per layer the input projection of every step as one fp16
  * MFMA GEMM (plh_input_projection's kernel; for layer 0 with input_size <= 32 at H > 256 inside the

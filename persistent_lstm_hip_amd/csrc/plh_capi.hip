@@ -212,6 +212,70 @@ void* scratch_ptr(hipError_t* err) {
   return ptr;
 }
 
+// Forwards on different streams of one device run one after the other.  Each persistent launch needs
+// all its workgroups co-resident; two launched from two streams at once would be dispatched
+// interleaved, each holding part of the device while waiting for its own undispatched workgroups,
+// until both time out.  While a device has seen forwards on one stream only, that stream orders
+// them and nothing else is done (an event record per forward costs ~3.5 us of the next launch).
+// The first forward on a second stream synchronises the device once (the earlier stream's handle
+// may be gone, so no event is recorded on it); from then on each forward waits (hipStreamWaitEvent)
+// for the device's last forward when that one was on another stream, and records an event after
+// its own launches.  Inside a stream capture nothing is waited for or recorded: the captured
+// graph's launches are ordered by whoever replays it.
+struct DeviceOrder {
+  std::mutex mu;
+  hipEvent_t done = nullptr;   // multi: recorded after the last forward's launches (never destroyed)
+  hipStream_t last = nullptr;  // the stream of the last forward (compared, never used)
+  bool any = false;            // a forward was enqueued
+  bool multi = false;          // forwards were enqueued on more than one stream
+};
+std::mutex g_order_mu;
+std::unordered_map<int, DeviceOrder*> g_order;  // one per device, never freed
+
+class StreamOrder {
+ public:
+  explicit StreamOrder(hipStream_t s) : s_(s) {
+    int dev = 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    err_ = hipGetDevice(&dev);
+    if (err_ == hipSuccess) err_ = hipStreamIsCapturing(s, &cs);
+    if (err_ != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+    {
+      std::lock_guard<std::mutex> lk(g_order_mu);
+      DeviceOrder*& o = g_order[dev];
+      if (!o) o = new DeviceOrder();
+      order_ = o;
+    }
+    lock_ = std::unique_lock<std::mutex>(order_->mu);
+    const bool other = order_->any && order_->last != s;
+    if (other && !order_->multi) {
+      if (!order_->done) err_ = hipEventCreateWithFlags(&order_->done, hipEventDisableTiming);
+      if (err_ == hipSuccess) err_ = hipDeviceSynchronize();
+      if (err_ != hipSuccess) return;
+      order_->multi = true;
+    } else if (other) {
+      err_ = hipStreamWaitEvent(s, order_->done, 0);
+      if (err_ != hipSuccess) return;
+    }
+    active_ = true;
+  }
+  hipError_t error() const { return err_; }
+  // After the forward's launches (also after a failed one: what it enqueued is ordered too).
+  ~StreamOrder() {
+    if (!active_) return;
+    if (order_->multi && hipEventRecord(order_->done, s_) != hipSuccess) return;
+    order_->last = s_;
+    order_->any = true;
+  }
+
+ private:
+  hipStream_t s_;
+  DeviceOrder* order_ = nullptr;
+  std::unique_lock<std::mutex> lock_;
+  hipError_t err_ = hipSuccess;
+  bool active_ = false;
+};
+
 }  // namespace
 
 extern "C" {
@@ -330,6 +394,8 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
   uint32_t* status = (uint32_t*)(ws + w.status);
   uint32_t* counters = (uint32_t*)(ws + w.counters);
 
+  StreamOrder order(s);
+  if (order.error() != hipSuccess) return fail_hip(order.error(), "ordering against other streams' forwards");
   if (batch == 0) {
     err = plh::launch_zero_u32(status, 1, s);
     return err == hipSuccess ? PLH_OK : fail_hip(err, "status reset");

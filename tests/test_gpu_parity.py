@@ -646,6 +646,36 @@ def test_sliced_side_stream_and_determinism(gpu):
     assert torch.equal(a, b) and torch.equal(a, c)
 
 
+@pytest.mark.parametrize("H,B", [(128, 512), (256, 512), (512, 512)])
+def test_forwards_on_two_streams_interleaved(gpu, H, B):
+    """Full-device launches enqueued alternately on two streams (each with its own workspace) and
+    never synchronised in between: the library orders them (each waits for the other stream's last
+    forward), so none ends partly resident and timed out; every result equals the single-stream one
+    bit for bit, and both streams' status words are clean.  H512 at B = 512 runs layer by layer."""
+    I, L, O, T = 5, 2, 6, 40
+    _say(f"two streams H={H} B={B}")
+    native = make_regressor(I, H, L, O)
+    model = _gpu_model(native)
+    xg = make_x(B, T, I).to("cuda", torch.float16)
+    ref = model(xg)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    outs = [[], []]
+    for _ in range(4):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                outs[i].append(model(xg))
+    for i, st in enumerate(streams):
+        with torch.cuda.stream(st):
+            gpu.check_status(torch.device("cuda"))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for o in outs[i]:
+            assert torch.equal(o, ref), f"stream {i}: result differs from the single-stream forward"
+
+
 def test_sliced_two_tile_workgroups_ragged_partial_launch(gpu):
     """H256, 4 layers, 600 rows: one-tile workgroups would need several launches, so each workgroup
     carries two software-pipelined tiles (512 rows per launch, then 88 rows with a padding tile), with

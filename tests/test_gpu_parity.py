@@ -676,6 +676,46 @@ def test_forwards_on_two_streams_interleaved(gpu, H, B):
             assert torch.equal(o, ref), f"stream {i}: result differs from the single-stream forward"
 
 
+def test_forwards_from_two_host_threads(gpu):
+    """Two host threads, each with its own stream, enqueue full-device forwards concurrently (the C
+    ABI runs without the GIL): the library's per-device ordering serialises them, and every result
+    equals the single-stream one bit for bit."""
+    import threading
+
+    I, H, L, O, B, T = 5, 128, 4, 24, 512, 40
+    _say("two host threads")
+    native = make_regressor(I, H, L, O)
+    model = _gpu_model(native)
+    xg = make_x(B, T, I).to("cuda", torch.float16)
+    ref = model(xg)
+    torch.cuda.synchronize()
+    outs, errors = [[], []], []
+
+    def work(i):
+        try:
+            st = torch.cuda.Stream()
+            with torch.cuda.stream(st):
+                for _ in range(6):
+                    outs[i].append(model(xg))
+                gpu.check_status(torch.device("cuda"))
+            st.synchronize()
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in threads), "a forward thread did not finish"
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert len(outs[i]) == 6
+        for o in outs[i]:
+            assert torch.equal(o, ref), f"thread {i}: result differs from the single-stream forward"
+
+
 def test_sliced_two_tile_workgroups_ragged_partial_launch(gpu):
     """H256, 4 layers, 600 rows: one-tile workgroups would need several launches, so each workgroup
     carries two software-pipelined tiles (512 rows per launch, then 88 rows with a padding tile), with

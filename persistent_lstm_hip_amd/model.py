@@ -194,6 +194,8 @@ class PersistentLSTM(nn.Module):
             x, lengths = pad_packed_sequence(x, batch_first=True)
         if not isinstance(x, torch.Tensor) or x.dim() != 3:
             raise ValueError("PersistentLSTM expects batch_first input [batch, seq_len, input_size]")
+        if x.size(1) == 0:
+            raise ValueError("expected sequence length to be larger than 0 (as nn.LSTM)")
         if x.device.type != "cuda":
             raise ValueError("PersistentLSTM runs on a HIP device only; move the input and module to 'cuda'")
         dtype = x.dtype
@@ -279,6 +281,8 @@ class PersistentLSTMRegressor(nn.Module):
     def _check_input(self, x: torch.Tensor) -> None:
         if not isinstance(x, torch.Tensor) or x.dim() != 3:
             raise ValueError("x must be a [batch, seq_len, input_size] tensor")
+        if x.size(1) == 0:
+            raise ValueError("expected sequence length to be larger than 0 (nn.LSTM refuses it too)")
         if x.device.type != "cuda":
             raise ValueError("PersistentLSTMRegressor runs on a HIP device only; move the input and module to 'cuda'")
 

@@ -141,6 +141,20 @@ def test_uniform_batch_mode_validation(monkeypatch):
     assert not conv._should_use_uniform_batch_fast_path(x)
 
 
+def test_empty_sequence_is_refused_like_nn_lstm():
+    """nn.LSTM refuses seq_len 0 ("Expected sequence length to be larger than 0"); so do the drop-ins,
+    before touching a device."""
+    native = make_regressor(5, 16, 2, 3)
+    with pytest.raises(RuntimeError):
+        native(torch.zeros(2, 0, 5))
+    conv = P.PersistentLSTMRegressor.from_native_module(native)
+    with pytest.raises(ValueError, match="sequence length"):
+        conv._check_input(torch.zeros(2, 0, 5))
+    lstm = P.PersistentLSTM.from_native_module(native.lstm)
+    with pytest.raises(ValueError, match="sequence length"):
+        lstm(torch.zeros(2, 0, 5))
+
+
 def test_kpairs_unpack_inverts_the_reference_packing():
     """model.py:20-27 packs W[4H, K] as P[p, c, j] = W[c, 2p + j] (zero-padded K); unpack is its inverse."""
     for k in (5, 8, 128):

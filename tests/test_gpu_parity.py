@@ -626,6 +626,24 @@ def test_edge_geometries(gpu, I, H, L, O, B, T, zero_tail):
                                    np.broadcast_to(native.linear.bias.detach().numpy(), (B - 16, O)), atol=2e-3)
 
 
+@pytest.mark.parametrize("H", [128, 512])
+def test_empty_batch(gpu, H):
+    """An empty batch gives empty outputs of nn.LSTM's shapes and launches nothing that reads x."""
+    I, L, O, T = 5, 2, 3, 7
+    _say(f"empty batch H={H}")
+    native = make_regressor(I, H, L, O)
+    x = torch.zeros(0, T, I, device="cuda", dtype=torch.float16)
+    out = _gpu_model(native)(x)
+    gpu.check_status(torch.device("cuda"))
+    assert tuple(out.shape) == (0, O)
+    with torch.inference_mode():
+        want_seq, (want_h, _) = native.lstm(torch.zeros(0, T, I))
+    mod = PersistentLSTM.from_native_module(native.lstm).to("cuda").half()
+    seq, (h_n, c_n) = mod(x)
+    assert tuple(seq.shape) == tuple(want_seq.shape) and tuple(h_n.shape) == tuple(want_h.shape)
+    assert tuple(c_n.shape) == tuple(want_h.shape)
+
+
 def test_sliced_side_stream_and_determinism(gpu):
     """H512 on a non-default stream (its own workspace) equals the default-stream result bit for bit."""
     I, H, L, O, B, T = 5, 512, 2, 6, 40, 30

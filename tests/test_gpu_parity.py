@@ -789,25 +789,32 @@ def test_kernel_timing_rearm(gpu):
     assert 0.0 < ms < a.elapsed_time(b), (ms, a.elapsed_time(b))
 
 
-def test_random_geometry_sweep(gpu):
+@pytest.mark.parametrize("seed,count,wide", [(20261203, 64, False), (777, 200, True)])
+def test_random_geometry_sweep(gpu, seed, count, wide):
     """Seeded random geometries through plh_forward: input size (also above the padded hidden size),
     hidden size 1..1024 (every kernel family, padded and unpadded), layers, head size (0 = no head),
     batch (above one 128-row launch at padded H 1024), length, ragged lengths with zeros, initial
     states and two probe steps.  Every output (head, sequence, final h/c, probed h/c) is checked
-    against the C oracle at the north-star tolerance."""
-    rng = np.random.default_rng(20261203)
+    against the C oracle at the north-star tolerance.  The wide draw also takes batches up to 700
+    (several launches, 16-row tiles at H <= 128), sequences up to 260, five layers and inputs up to
+    1200."""
+    rng = np.random.default_rng(seed)
     device = torch.device("cuda")
     done = 0
-    while done < 64:
-        I = int(rng.integers(1, 41)) if rng.random() < 0.8 else int(rng.integers(41, 700))
+    while done < count:
+        I = int(rng.integers(1, 41)) if rng.random() < 0.8 else int(rng.integers(41, 1200 if wide else 700))
         u = rng.random()
         H = int(rng.integers(1, 129)) if u < 0.4 else int(rng.integers(129, 513)) if u < 0.75 else \
             int(rng.integers(513, 1025))
-        L = int(rng.integers(1, 5))
+        L = int(rng.integers(1, 6 if wide else 5))
         O = 0 if rng.random() < 0.2 else int(rng.integers(1, 31))
-        B = int(rng.integers(1, 71)) if H <= 512 else int(rng.integers(1, 161))
-        T = int(rng.integers(1, 121))
-        if B * T * L * 4 * H * (I + H) > 4e8:
+        if wide:
+            B = int(rng.integers(1, 700)) if H <= 128 else int(rng.integers(1, 330))
+            T = int(rng.integers(1, 261))
+        else:
+            B = int(rng.integers(1, 71)) if H <= 512 else int(rng.integers(1, 161))
+            T = int(rng.integers(1, 121))
+        if B * T * L * 4 * H * (I + H) > (1e9 if wide else 4e8):
             continue  # keep the oracle to a fraction of a second per case
         ragged = rng.random() < 0.5
         with_state = rng.random() < 0.5

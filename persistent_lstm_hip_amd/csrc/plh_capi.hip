@@ -62,6 +62,7 @@ struct Plan {
   int chunk_rows = 16;
   int wg_tiles = 1;  // sliced: 16-row tiles per workgroup
   bool rec = false;  // layer-sequential path (plh::as_layer_sequential)
+  bool fits = true;  // the workgroups of one tile fit the device at once
 };
 
 Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
@@ -77,6 +78,7 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
   // keeps the XCD-aware mapping available.  A sliced workgroup carries two software-pipelined tiles
   // (where the kernel allows it) only when one tile each would need more than one launch.
   int groups = cap16 / (g.rec ? g.slices : g.L * g.slices);
+  p.fits = groups >= 1;
   if (groups >= 8) groups &= ~7;
   groups = std::max(1, groups);
   const int tiles16 = (batch + 15) / 16;
@@ -106,7 +108,9 @@ Plan plan_path(const plh::Geometry& g, int batch, bool need_device, hipError_t* 
 // to 512 rows of one layer (plus one projection GEMM per layer after the first).  The
 // layer-sequential path is used when the batch needs more wavefront launches than there are layers
 // (so it does fewer launches of recurrent steps), and only while its workspace - a layer's
-// projections for every step, ~4 MB per step at 512 rows - stays within kMaxSeqWorkspace.
+// projections for every step, ~4 MB per step at 512 rows - stays within kMaxSeqWorkspace.  It is also
+// used whenever one tile of all L layers does not fit the device (L x 16 slices > the co-resident
+// workgroups: more than 16 layers at padded H 512).
 constexpr size_t kMaxSeqWorkspace = (size_t)24 << 30;
 Plan plan_for(const plh::Geometry& g, int batch, int seq_len, bool need_device, hipError_t* err) {
   if (!g.wave_ok) {
@@ -122,6 +126,7 @@ Plan plan_for(const plh::Geometry& g, int batch, int seq_len, bool need_device, 
   if (*err != hipSuccess) return p;
   q.rec = true;
   if (plh::workspace_layout(gr, seq_len, q.chunk_rows, q.tile_rows).total > kMaxSeqWorkspace) return p;
+  if (!p.fits) return q;
   const long long n_wave = (std::max(batch, 1) + (long long)p.chunk_rows - 1) / p.chunk_rows;
   return n_wave > g.L ? q : p;
 }

@@ -154,6 +154,24 @@ def test_layer_sequential_workspace_layout(ext):
     assert wave <= b < wave + (1 << 12)
 
 
+def test_deep_h512_stacks_go_layer_by_layer(ext):
+    # One tile of the sliced path takes L x 16 workgroups at padded H 512: beyond 16 layers it would
+    # not fit 256 co-resident workgroups, so the layer-sequential path (8 per tile) serves even small
+    # batches.  Its workspace: one layer's projections [T][rows][4 HP], two layer-input buffers, the
+    # ring of 2 tiles (32 rows) and x packed for layer 0's in-kernel projection.
+    T, rows, H = 6, 32, 512
+    gates = T * rows * 4 * H * 2
+    xs = 2 * T * rows * H * 2
+    ring = (rows // 16) * (2 * H * 8 * 8 + 16 * 8)
+    xp = rows * T * 64
+    for L in (17, 40, 64):
+        b = ext.workspace_bytes(5, H, L, 3, 20, T)
+        assert gates + xs + ring + xp <= b < gates + xs + ring + xp + (1 << 12), L
+    # 16 layers still fit one sliced tile: the wavefront path keeps the small batch
+    sliced = ext.workspace_bytes(5, H, 16, 3, 20, T)
+    assert sliced >= 15 * 16 * T * H * 2  # the (L-1)-layer hand-off of one 16-row tile
+
+
 def test_wide_hidden_and_input_workspace_layout(ext):
     # H 513..1024 (padded 1024): only the layer-sequential path; 32 slices of 32 units per 16-row tile,
     # so 256 / 32 = 8 tiles (128 rows) per launch.  I <= 32: x packed for layer 0's in-kernel projection.

@@ -626,6 +626,26 @@ def test_edge_geometries(gpu, I, H, L, O, B, T, zero_tail):
                                    np.broadcast_to(native.linear.bias.detach().numpy(), (B - 16, O)), atol=2e-3)
 
 
+@pytest.mark.parametrize("I,H,L,O,B,T", [
+    (5, 128, 64, 3, 20, 6),      # 64 layers (the limit): wavefront, 8-row tiles
+    (5, 256, 64, 3, 20, 6),      # 64 layers of 4 slices: one tile fills the device
+    (5, 512, 17, 3, 20, 6),      # padded H 512 beyond 16 layers: one tile would not fit the sliced
+    (5, 300, 64, 3, 9, 4),       # path, so the layer-sequential path runs it (also at I <= 32, B = 9)
+    (5, 64, 2, 4096, 12, 5),     # the largest head
+    (65536, 64, 2, 7, 4, 3),     # the largest input: layer 0's projection GEMM over K = 65536
+])
+def test_limit_geometries(gpu, I, H, L, O, B, T):
+    """Geometries at the documented limits (64 layers, head 4096, input 65536) and deep stacks at
+    padded H 512, whose tiles only the layer-sequential path can hold, against the oracle."""
+    _say(f"limits I={I} H={H} L={L} O={O} B={B} T={T}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    got = _gpu_model(native)(x.to("cuda", torch.float16))
+    gpu.check_status(torch.device("cuda"))
+    want = oracle.regressor_forward(x.numpy(), oracle_layers(native.lstm), *linear_params(native.linear))
+    assert_close(got.float().cpu().numpy(), want, what="limit geometry out")
+
+
 @pytest.mark.parametrize("H", [128, 512])
 def test_empty_batch(gpu, H):
     """An empty batch gives empty outputs of nn.LSTM's shapes and launches nothing that reads x."""

@@ -646,6 +646,26 @@ def test_limit_geometries(gpu, I, H, L, O, B, T):
     assert_close(got.float().cpu().numpy(), want, what="limit geometry out")
 
 
+@pytest.mark.parametrize("H,B", [(128, 16), (256, 8)])
+def test_long_sequence_drift(gpu, H, B):
+    """Ten thousand steps (ten times the north star's): h and c of every layer after 1, 5000 and 10000
+    steps and the head stay within the bound against the fp32 oracle (fp16 h storage does not
+    accumulate into drift)."""
+    I, L, O, T = 5, 4, 24, 10000
+    _say(f"long sequence H={H} B={B} T={T}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    model = _gpu_model(native)
+    out, ph, pc = model.forward_probe(x.to("cuda", torch.float16), [1, 5000, 10000])
+    gpu.check_status(torch.device("cuda"))
+    ref = oracle.lstm_forward(x.numpy(), oracle_layers(native.lstm), probe_steps=(1, 5000, 10000))
+    for p, step in enumerate((1, 5000, 10000)):
+        assert_close(ph[p].cpu().numpy(), ref["probe_h"][p], what=f"h after {step} steps")
+        assert_close(pc[p].cpu().numpy(), ref["probe_c"][p], what=f"c after {step} steps")
+    want = oracle.linear(ref["h_n"][-1], *linear_params(native.linear))
+    assert_close(out.float().cpu().numpy(), want, what="head after 10000 steps")
+
+
 @pytest.mark.parametrize("H", [128, 512])
 def test_empty_batch(gpu, H):
     """An empty batch gives empty outputs of nn.LSTM's shapes and launches nothing that reads x."""

@@ -197,6 +197,137 @@ proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* 
   }
 }
 
+// The blocked layouts at K = 32 KS (KS = 4, 8 or 16: K = 128, 256, 512), with the k-steps of an m-tile
+// unrolled at compile time.  The same work split, W slice and X ring as proj_gemm_kernel, written so
+// that the compiler keeps the ring's loads kRing - 1 steps ahead everywhere: with a runtime k-loop the
+// register allocator rotated the ring slots through the accumulators and waited for every
+// outstanding load (vmcnt(0) / vmcnt(1)) twice per four k-steps.  Here
+//   * X and C go through buffer descriptors of the wave's 64 rows, so a load or store is one
+//     instruction with a scalar offset (16-row block a, k-chunk kc) and the lane's 16-byte offset:
+//     no per-load 64-bit address arithmetic; blocks at or past M / 16 fall outside the descriptor,
+//     so their loads read zeros and their stores are dropped (no clamping);
+//   * the W fragments of a k-step are read from LDS two ahead of the MFMAs that use them (3 live
+//     instead of 8), and scheduling groups fix each step's issue order: the ring's 4 loads, 2 W
+//     reads, then 6 x (4 MFMAs, 1 W read) and 8 MFMAs.
+// [512000,512]x[512,2048] 1.03-1.05 -> 0.966-0.98 ms, [512000,128]x[128,512] 0.117 -> 0.109 ms
+// (interleaved runs on one box each).
+template <int KS>
+__global__ void __launch_bounds__(kGemmThreads)
+proj_gemm_blocked_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* __restrict__ W,
+                         _Float16* __restrict__ C, long long ldc, int M, int tiles_m, int n_slices, int m_groups) {
+  static_assert(kGemmWaves == 8 && kGemmWM == 4 && KS % kRing == 0 && KS * 32 <= kGemmMaxK, "tile shape");
+  constexpr int K = 32 * KS;
+  __shared__ f16x8 wl[KS * 8 * 64];  // [k-chunk][n-tile 0..7][64 lanes] f16x8
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+  const int ns = idx % n_slices;
+  const int mg = (idx / n_slices) * 8 + xcd;
+  if (mg >= m_groups) return;
+  const int n0 = ns * kGemmBN;
+  for (int e = threadIdx.x; e < KS * 8 * 64; e += kGemmThreads) {
+    const int l = e & 63, nt = (e >> 6) & 7, kc = e >> 9;
+    const int n = n0 + gemm_w_row(nt, l & 15);
+    wl[e] = *reinterpret_cast<const f16x8*>(W + (size_t)n * K + kc * 32 + (l >> 4) * 8);
+  }
+  __syncthreads();
+  int mt = mg;
+  if (mt >= tiles_m) return;
+  const int nblk = M / 16;
+  const int xa = (int)(ldx * 32), ca = (int)(ldc * 32);  // bytes from one 16-row block to the next
+  // 16-row blocks a descriptor may span (its byte count is a 31-bit number)
+  const int max_xb = 0x7FFFFFFF / xa, max_cb = 0x7FFFFFFF / ca;
+  // X rows of m-tile t held by this wave: blocks 32 t + 4 wave .. + 3
+  auto xrs = [&](int t) {
+    const int mb = t * (kGemmBM / 16) + wave * kGemmWM;
+    const int nb = min(max(nblk - mb, 0), max_xb);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(X) + (size_t)(mb < nblk ? mb : 0) * ldx * 16, 0,
+                                             nb * xa, 0x00020000);
+  };
+  const unsigned voff = (unsigned)lane * 16u;
+  f16x8 xr[kRing][kGemmWM];
+  auto ld = [&](__amdgpu_buffer_rsrc_t rs, int kc, f16x8 (&dst)[kGemmWM]) {
+#pragma unroll
+    for (int a = 0; a < kGemmWM; ++a)
+      dst[a] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, a * xa + kc * 1024, 0));
+  };
+  {
+    // In ring order, as the loop's last steps issue them for the next tile: the loop header's waits
+    // are the tighter of the two paths into it, and a slot loaded last here would make every tile's
+    // first step wait for the previous tile's result stores.
+    const auto rs = xrs(mt);
+#pragma unroll
+    for (int j = 0; j < kRing - 1; ++j) {
+      ld(rs, j, xr[j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  for (;;) {
+    const int nmt = mt + m_groups;
+    const int pmt = nmt < tiles_m ? nmt : mt;  // prefetch target past the last tile: reload this one
+    const auto rc = xrs(mt), rn = xrs(pmt);
+    f32x4 acc[kGemmWM][8];
+#pragma unroll
+    for (int a = 0; a < kGemmWM; ++a)
+#pragma unroll
+      for (int b = 0; b < 8; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        const int sn = s + kRing - 1;  // this tile's step sn, or the next tile's first steps
+        if (sn < KS)
+          ld(rc, sn, xr[sn % kRing]);
+        else
+          ld(rn, sn - KS, xr[sn % kRing]);
+      }
+      f16x8 wa[3];
+      wa[0] = wl[(s * 8 + 0) * 64 + lane];
+      wa[1] = wl[(s * 8 + 1) * 64 + lane];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        if (b + 2 < 8) wa[(b + 2) % 3] = wl[(s * 8 + b + 2) * 64 + lane];
+#pragma unroll
+        for (int a = 0; a < kGemmWM; ++a)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[b % 3], xr[s % kRing][a], acc[a][b], 0, 0, 0);
+      }
+      // issue order (masks: 0x020 vector-memory reads, 0x100 LDS reads, 0x008 MFMA)
+      __builtin_amdgcn_sched_group_barrier(0x020, kGemmWM, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int g = 0; g < 6; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, kGemmWM, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * kGemmWM, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      // the tile's result: blocks 32 mt + 4 wave + a, column blocks n0 / 32 + p; rows at or past M
+      // fall outside the descriptor
+      const int mb = mt * (kGemmBM / 16) + wave * kGemmWM;
+      const int rem = max(min(max(nblk - mb, 0), max_cb) * ca - n0 * 32, 0);
+      const auto rs = __builtin_amdgcn_make_buffer_rsrc(C + (mb < nblk ? (size_t)mb * ldc * 16 + (size_t)n0 * 16 : 0), 0,
+                                                        rem, 0x00020000);
+#pragma unroll
+      for (int a = 0; a < kGemmWM; ++a)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          f16x8 v;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v[j] = (_Float16)acc[a][2 * p][j];
+            v[4 + j] = (_Float16)acc[a][2 * p + 1][j];
+          }
+          // nontemporal (cache policy 2), as in proj_gemm_kernel
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v),
+                                                 rs, voff, a * ca + p * 1024, 2);
+        }
+    }
+    if (nmt >= tiles_m) break;
+    mt = nmt;
+  }
+}
+
 }  // namespace
 
 bool gemm_shape_ok(long long M, int N, int K, long long ldx, long long ldc, bool blocked) {
@@ -214,6 +345,16 @@ hipError_t launch_proj_gemm(const _Float16* X, long long ldx, const _Float16* W,
   // m-tile), placed so that an m-group's slices share an XCD.
   const int m_groups = std::max(1, std::min(tiles_m, std::max(cus, 1) / n_slices));
   const int grid = ((m_groups + 7) / 8) * 8 * n_slices;
+  // The compile-time-K kernel where one is built (at K = 384 it spills, and the generic kernel runs).
+  auto* fk = !blocked || ldc > (1 << 20) ? nullptr
+             : K == 128                   ? proj_gemm_blocked_kernel<4>
+             : K == 256                   ? proj_gemm_blocked_kernel<8>
+             : K == 512                   ? proj_gemm_blocked_kernel<16>
+                                          : nullptr;
+  if (fk) {
+    hipLaunchKernelGGL(fk, dim3(grid), dim3(kGemmThreads), 0, s, X, ldx, W, C, ldc, (int)M, tiles_m, n_slices, m_groups);
+    return hipGetLastError();
+  }
   const bool kb = K > kGemmMaxK;
   auto* fn = blocked ? (kb ? proj_gemm_kernel<true, true> : proj_gemm_kernel<true, false>)
                      : (kb ? proj_gemm_kernel<false, true> : proj_gemm_kernel<false, false>);

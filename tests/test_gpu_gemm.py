@@ -47,6 +47,9 @@ def test_input_projection_matches_float64(gpu, M, K, N, pad):
     (4000, 128, 512, 128),     # the C2 layer shape
     (1616, 384, 2048, 512),    # H = 300 padded to 384 within a 512-wide layer buffer; 101 row blocks
     (128000, 1024, 4096, 1024),  # the H 1024 layer shape of one 128-row launch, T = 1000 (two K blocks)
+    (1040, 256, 384, 256),     # 65 row blocks: the last tile's waves hold 1 and 0 valid blocks
+    (5008, 512, 1024, 1024),   # x rows wider than K (NaN past K), a partial last tile
+    (16, 128, 128, 128),       # a single row block
 ])
 def test_input_projection_blocked_layout(gpu, M, K, N, ldx):
     """Fragment-blocked x and out (the layout the layer-sequential path keeps): the result equals the

@@ -345,6 +345,24 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
                                : reinterpret_cast<f16x8*>(a.hout) + ((size_t)tile * (HP / 32) + (copy_k8 >> 2)) * 64 +
                                      (copy_k8 & 3) * 16 + copy_row;
   auto copy_out = [&](int t, const f16x8& v) { copy_dst[(size_t)t * a.ntile * (HP / 32) * 64] = v; };
+  // The same copy inside the step loop (NJ = 2), as one 16-byte buffer store by every thread on every path:
+  // a descriptor of step t's layer input (no bytes in the last layer), and threads past the copy
+  // address it out of range, so their store is dropped.  The gather's wait for the ring poll then
+  // leaves this store in flight (vmcnt(1)); with the store on some paths only, the compiler merged the
+  // paths into a wait for every access in flight (vmcnt(0)), this store's completion included.
+  const size_t copy_step = (size_t)a.ntile * (HP / 32) * 64;  // f16x8 per step of the layer input
+  const unsigned copy_off =
+      threadIdx.x < kCopyThreads
+          ? (unsigned)((((size_t)tile * (HP / 32) + (copy_k8 >> 2)) * 64 + (copy_k8 & 3) * 16 + copy_row) * 16)
+          : 0xFFFFFFF0u;
+  auto copy_out_step = [&](int t, const f16x8& v) {
+    const bool any = !last && t >= 0;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        any ? reinterpret_cast<f16x8*>(a.hout) + (size_t)(any ? t : 0) * copy_step : nullptr, 0,
+        any ? (int)(copy_step * 16) : 0, 0x00020000);
+    typedef unsigned int u32x4c __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4c, v), rs, copy_off, 0, 0);
+  };
   // One step: h_{t-1} in hbuf[t & 1] -> h_t in hbuf[(t + 1) & 1]; gp holds the input projection of
   // step t (X0: x_t) on entry and that of step t + 1 on return.  Returns false if a wait failed.
   // Step t + 1's projection is loaded first: it retires before this step's ring poll (loads retire
@@ -491,9 +509,12 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       own32[own_dst] = xw_dec_pair(pair_lo);
       own32[own_dst + (NJ == 2 ? 2 : 1)] = xw_dec_pair(pair_hi);
     }
-    if (!last) {
-      if (threadIdx.x < kCopyThreads && t > 0) copy_out(t - 1, hcp);
-    } else if (a.out_seq && row_ok) {
+    if constexpr (NJ == 2) {
+      copy_out_step(t - 1, hcp);
+    } else if (!last && threadIdx.x < kCopyThreads && t > 0) {
+      copy_out(t - 1, hcp);  // (at padded H 1024 the store on every path measured 1.2% slower)
+    }
+    if (last && a.out_seq && row_ok) {
       _Float16* dst = a.out_seq + ((size_t)grow * a.T + t) * a.H + eu;
 #pragma unroll
       for (int j = 0; j < NJ; ++j)

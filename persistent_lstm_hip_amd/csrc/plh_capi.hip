@@ -63,6 +63,7 @@ struct Plan {
   int wg_tiles = 1;  // sliced: 16-row tiles per workgroup
   bool rec = false;  // layer-sequential path (plh::as_layer_sequential)
   bool fits = true;  // the workgroups of one tile fit the device at once
+  bool pad8 = false; // the co-resident tiles are a multiple of 8: a launch may round its grid up to 8 tiles
 };
 
 Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
@@ -80,6 +81,7 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
   int groups = cap16 / (g.rec ? g.slices : g.L * g.slices);
   p.fits = groups >= 1;
   if (groups >= 8) groups &= ~7;
+  p.pad8 = groups % 8 == 0;
   groups = std::max(1, groups);
   const int tiles16 = (batch + 15) / 16;
   const int wt = (g.slices > 1 && g.max_wg_tiles > 1 && tiles16 > groups) ? g.max_wg_tiles : 1;
@@ -452,7 +454,12 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     a.wg_tiles = plan.wg_tiles;
     a.ntile = (a.ntile + a.wg_tiles - 1) / a.wg_tiles * a.wg_tiles;
     a.rows_pad = a.ntile * plan.tile_rows;
-    a.xcd_map = ((g.slices > 1 && !g.rec) ? (g.L * a.ntile / a.wg_tiles) % 8 : a.ntile % 8) == 0 ? 1 : 0;
+    // Layer by layer, the grid covers a multiple of 8 tiles where the device holds that many (the
+    // extra workgroups exit at once), so that every tile's slices share an XCD and exchange h through
+    // its L2 whatever the batch: without it, B = 320 and 448 (20 and 28 tiles) took 10.2 and 11.2 ms
+    // at H 512 against 9.3 ms at B = 384 (24 tiles).
+    a.ntile_grid = g.rec && plan.pad8 ? (a.ntile + 7) / 8 * 8 : a.ntile;
+    a.xcd_map = ((g.slices > 1 && !g.rec) ? (g.L * a.ntile / a.wg_tiles) % 8 : a.ntile_grid % 8) == 0 ? 1 : 0;
     if (g.rec) {
       // Layer by layer.  Layer 0: with I <= 32 its input projection runs inside the recurrent kernel
       // from x packed by the prologue; otherwise x goes to xs slot 0 for the projection GEMM.  Every

@@ -131,6 +131,8 @@ struct ForwardArgs {
   int wg_tiles;                 // sliced kernels: 16-row tiles per workgroup (1 or 2); ntile is a multiple
   // layer-sequential kernel (one layer per launch):
   int layer;                    // the layer this launch runs
+  int ntile_grid;               // tiles the launch's grid covers (>= ntile: a multiple of 8 where that fits,
+                                // so that every tile's slices share an XCD); the extra ones exit at once
   const _Float16* gates;        // [T * rows_pad][4 HP] blocked: input projection of that layer (no bias), lane order
   _Float16* hout;               // [T * rows_pad][HP] blocked: its h sequence, the next layer's input (null: last layer)
   const _Float16* wx0;          // rec_x0, layer 0: W_ih fragments of the in-kernel projection (x from xp)

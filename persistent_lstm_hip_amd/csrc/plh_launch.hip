@@ -1,5 +1,7 @@
 // plh_launch.hip -- host side of the kernels: geometry rules, buffer layouts, kernel choice,
 // occupancy and the launch of the persistent recurrence.
+#include <algorithm>
+
 #include "plh_device.h"
 
 namespace plh {
@@ -147,7 +149,7 @@ hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t
   ForwardArgs args = a;
   void* params[] = {&args};
   // One layer per launch (layer-sequential) or every layer of the chunk at once.
-  const unsigned grid = g.rec ? a.ntile * g.slices : a.L * a.ntile / a.wg_tiles * g.slices;
+  const unsigned grid = g.rec ? std::max(a.ntile, a.ntile_grid) * g.slices : a.L * a.ntile / a.wg_tiles * g.slices;
   // An ordinary launch on the stream's own queue.  Co-residency of the grid comes from the caller:
   // plh_forward sizes every launch to at most the occupancy-derived capacity (recurrent_capacity),
   // and the launch starts after the stream's previous kernels have finished, so every workgroup is

@@ -160,8 +160,10 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  int unused_layer, tile, slice;
-  sliced_coords(blockIdx.x, a.ntile, S, a.xcd_map, unused_layer, tile, slice);
+  int grid_layer, tile, slice;
+  sliced_coords(blockIdx.x, a.ntile, S, a.xcd_map, grid_layer, tile, slice);
+  // Workgroups of the tiles that only round the grid up to a multiple of 8 (whole tiles per XCD).
+  if (grid_layer != 0) return;
   const int layer = a.layer;
   const int en = lane & 15, kgx = lane >> 4;
   // This lane's units eu + 4 j (j < NJ) of row en: the D fragments of the wave's tiles (all four

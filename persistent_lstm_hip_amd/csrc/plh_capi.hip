@@ -64,6 +64,7 @@ struct Plan {
   bool rec = false;  // layer-sequential path (plh::as_layer_sequential)
   bool fits = true;  // the workgroups of one tile fit the device at once
   bool pad8 = false; // the co-resident tiles are a multiple of 8: a launch may round its grid up to 8 tiles
+  int cap_wgs = 0;   // co-resident workgroups (16-row tiles)
 };
 
 Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
@@ -82,6 +83,7 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
   p.fits = groups >= 1;
   if (groups >= 8) groups &= ~7;
   p.pad8 = groups % 8 == 0;
+  p.cap_wgs = cap16;
   groups = std::max(1, groups);
   const int tiles16 = (batch + 15) / 16;
   const int wt = (g.slices > 1 && g.max_wg_tiles > 1 && tiles16 > groups) ? g.max_wg_tiles : 1;
@@ -458,8 +460,12 @@ int plh_forward(const void* packed_dev, int input_size, int hidden_size, int num
     // extra workgroups exit at once), so that every tile's slices share an XCD and exchange h through
     // its L2 whatever the batch: without it, B = 320 and 448 (20 and 28 tiles) took 10.2 and 11.2 ms
     // at H 512 against 9.3 ms at B = 384 (24 tiles).
+    // The all-layers sliced kernel likewise rounds its (layer, tile group) groups up to a multiple
+    // of 8 where the device holds them (H256 B200: 1.92 ms against 1.47 at B192).
     a.ntile_grid = g.rec && plan.pad8 ? (a.ntile + 7) / 8 * 8 : a.ntile;
-    a.xcd_map = ((g.slices > 1 && !g.rec) ? (g.L * a.ntile / a.wg_tiles) % 8 : a.ntile_grid % 8) == 0 ? 1 : 0;
+    const int groups = g.L * a.ntile / a.wg_tiles, groups8 = (groups + 7) / 8 * 8;
+    a.groups_grid = g.slices > 1 && !g.rec && groups8 * g.slices <= plan.cap_wgs ? groups8 : groups;
+    a.xcd_map = ((g.slices > 1 && !g.rec) ? a.groups_grid % 8 : a.ntile_grid % 8) == 0 ? 1 : 0;
     if (g.rec) {
       // Layer by layer.  Layer 0: with I <= 32 its input projection runs inside the recurrent kernel
       // from x packed by the prologue; otherwise x goes to xs slot 0 for the projection GEMM.  Every

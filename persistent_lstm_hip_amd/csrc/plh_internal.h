@@ -133,6 +133,8 @@ struct ForwardArgs {
   int layer;                    // the layer this launch runs
   int ntile_grid;               // tiles the launch's grid covers (>= ntile: a multiple of 8 where that fits,
                                 // so that every tile's slices share an XCD); the extra ones exit at once
+  int groups_grid;              // sliced kernels: (layer, tile group) groups the grid covers (>= L ntile /
+                                // wg_tiles, rounded up to 8 the same way; 0: exactly those)
   const _Float16* gates;        // [T * rows_pad][4 HP] blocked: input projection of that layer (no bias), lane order
   _Float16* hout;               // [T * rows_pad][HP] blocked: its h sequence, the next layer's input (null: last layer)
   const _Float16* wx0;          // rec_x0, layer 0: W_ih fragments of the in-kernel projection (x from xp)

@@ -149,7 +149,9 @@ hipError_t launch_recurrent(const Geometry& g, const ForwardArgs& a, hipStream_t
   ForwardArgs args = a;
   void* params[] = {&args};
   // One layer per launch (layer-sequential) or every layer of the chunk at once.
-  const unsigned grid = g.rec ? std::max(a.ntile, a.ntile_grid) * g.slices : a.L * a.ntile / a.wg_tiles * g.slices;
+  const unsigned grid = g.rec            ? std::max(a.ntile, a.ntile_grid) * g.slices
+                        : g.slices > 1     ? std::max(a.L * a.ntile / a.wg_tiles, a.groups_grid) * g.slices
+                                           : a.L * a.ntile;
   // An ordinary launch on the stream's own queue.  Co-residency of the grid comes from the caller:
   // plh_forward sizes every launch to at most the occupancy-derived capacity (recurrent_capacity),
   // and the launch starts after the stream's previous kernels have finished, so every workgroup is

@@ -71,6 +71,8 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   const int lane = threadIdx.x & 63;
   int layer, tgrp, slice;
   sliced_coords(blockIdx.x, a.ntile / NTI, S, a.xcd_map, layer, tgrp, slice);
+  // Workgroups of the groups that only round the grid up to a multiple of 8 (whole groups per XCD).
+  if (layer >= a.L) return;
   const int en = lane & 15, kgx = lane >> 4;
   // This lane's units eu + 4 j (j < NJ) of row en: all four gates of each are in its D fragments.
   const int eu = slice * HS + wave * UPW + kgx;

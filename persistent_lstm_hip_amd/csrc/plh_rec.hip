@@ -492,15 +492,20 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // A first poll that finds a sibling's word not yet written costs a round trip (~800 cycles
     // under load), so every wave waits before polling: the first wave of each SIMD (waves 0-3)
     // finishes its cell updates ~500 cycles before the second (the matrix core serves the older
-    // wave first) and waits 896 cycles, the second 384.  The branch is on a wave-uniform value:
-    // s_sleep ignores the exec mask, so under a lane-masked branch every wave would sleep.  In
-    // interleaved C4 runs on two boxes: no wait 12.23 ms, 512 cycles for all waves 11.92 / 11.48,
-    // 512 for waves 0-3 only 12.01, 896 / 384 11.27-11.85 (-1.8% to -2.4%); 768-1152 / 256-384 within
-    // 1% of it.  Only the poll is delayed.
+    // wave first) and waits longer.  The branch is on a wave-uniform value: s_sleep ignores the exec
+    // mask, so under a lane-masked branch every wave would sleep.  Only the poll is delayed.  The
+    // delays (units of 64 cycles) are per padded H, from interleaved runs on one box each: 14 / 6
+    // had been chosen at C4 when the layer-input store still held up the poll's wait (no wait 12.23
+    // ms, 512 cycles for all waves 11.48-11.92, 14 / 6 11.27-11.85); after it, H512 B320 8.36 ->
+    // 8.02 ms and B448 9.13 -> 8.95 ms at 10 / 4 (8 / 2: 7.98 and 9.02), I300 H256 7.55 -> 7.17 ms at
+    // 8 / 2 (10 / 4: 7.24), H1024 41.9 -> 41.45 ms at 12 / 2 (10 / 4: 41.65); C4 within the noise
+    // of the box (-1.4% to -1.8% at 10 / 4 on three others).
+    constexpr int kPollSleepFirst = HP >= 1024 ? 12 : HP == 512 ? 10 : 8;
+    constexpr int kPollSleepSecond = HP == 512 ? 4 : 2;
     if (__builtin_amdgcn_readfirstlane(wave) < 4)
-      __builtin_amdgcn_s_sleep(14);
+      __builtin_amdgcn_s_sleep(kPollSleepFirst);
     else
-      __builtin_amdgcn_s_sleep(6);
+      __builtin_amdgcn_s_sleep(kPollSleepSecond);
 #pragma unroll
     for (int p = 0; p < NL; ++p)
       if (has_ld(p)) pload(p);

@@ -255,6 +255,29 @@ def test_large_batches_use_16_row_tiles_and_split_launches(gpu, B, T):
     assert_close(got.float().cpu().numpy()[rows], ref, what=f"B={B} vs oracle")
 
 
+@pytest.mark.parametrize("H,L,B,T", [
+    (256, 4, 200, 60),    # sliced, 13 tiles x 4 layers = 52 groups: grid rounded up to 56
+    (256, 3, 400, 30),    # sliced, two tiles per workgroup, 13 tile groups x 3 layers = 39 -> 40
+    (512, 2, 48, 40),     # sliced at H 512, 3 tiles x 2 layers = 6 groups -> 8
+    (512, 2, 320, 30),    # layer-sequential, 20 tiles -> 24
+    (1000, 2, 200, 12),   # layer-sequential at padded H 1024, 13 tiles: launches of 8 and 5 -> 8
+])
+def test_grids_rounded_up_to_whole_xcds(gpu, H, L, B, T):
+    """Batches whose tile (or tile group) count is not a multiple of 8 launch a grid rounded up to one,
+    whose extra workgroups return at once: every row against torch fp32, rows at both ends and the
+    middle against the oracle, and the extra workgroups leave the status word clear."""
+    I, O = 5, 16
+    _say(f"rounded-up grid H={H} L={L} B={B} T={T}")
+    native = make_regressor(I, H, L, O)
+    x = make_x(B, T, I)
+    got = _gpu_model(native)(x.to("cuda", torch.float16))
+    gpu.check_status(torch.device("cuda"))
+    assert_close(got.float().cpu().numpy(), _torch_ref(native, x), what=f"H={H} B={B}")
+    rows = np.r_[0:4, B // 2:B // 2 + 4, B - 4:B]
+    ref = oracle.regressor_forward(x.numpy()[rows], oracle_layers(native.lstm), *linear_params(native.linear))
+    assert_close(got.float().cpu().numpy()[rows], ref, what=f"H={H} B={B} vs oracle")
+
+
 @pytest.mark.parametrize("H", [256, 512])
 def test_large_hidden_c3_c4(gpu, H):
     """C3 (H256) and C4 (H512): 4 layers, B512, T1000.  C3 runs the sliced kernel (two tiles per

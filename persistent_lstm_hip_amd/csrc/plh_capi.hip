@@ -82,7 +82,7 @@ Plan make_plan(const plh::Geometry& g, int batch, int cap8, int cap16) {
   int groups = cap16 / (g.rec ? g.slices : g.L * g.slices);
   p.fits = groups >= 1;
   if (groups >= 8) groups &= ~7;
-  p.pad8 = groups % 8 == 0;
+  p.pad8 = groups >= 8;  // (then a multiple of 8)
   p.cap_wgs = cap16;
   groups = std::max(1, groups);
   const int tiles16 = (batch + 15) / 16;

@@ -172,7 +172,7 @@ def input_projection_timing(ext, dev, reps: int = 20, warmup: int = 5) -> dict:
                     "torch_mm_ms": ms_vendor, "speedup_vs_torch_mm": ms_vendor / ms})
         del x, w, wt, out
     torch.cuda.empty_cache()
-    return {"kernel": "proj_gemm_kernel<true> (plh_gemm.hip)", "measured": res,
+    return {"kernel": "proj_gemm_blocked_kernel<K/32> (plh_gemm.hip)", "measured": res,
             "note": "timed alone with HIP events; C2 itself computes each step's projection inside the "
                     "persistent wavefront kernel, C4 runs this GEMM for layers 1-3 (layer 0 in-kernel); "
                     "torch_mm_ms: torch.mm on the same operands (row-major), timed the same way"}

@@ -911,3 +911,62 @@ def test_random_geometry_sweep(gpu, seed, count, wide):
             w_head = oracle.linear(want["h_n"][-1], *linear_params(head))
             assert_close(res["out"].float().cpu().numpy(), w_head, what=f"{tag} head")
         done += 1
+
+
+@pytest.mark.parametrize("seed,count", [(31, 150)])
+def test_random_large_batch_sweep(gpu, seed, count):
+    """Seeded random geometries at batch sizes up to 1500 (H <= 128) and 800 (every other H up to
+    1024): several launches, 16-row tiles, padded grids and the layer-sequential path at batches the
+    whole-batch sweep does not reach.  The GPU runs the whole batch; the oracle runs the first, the
+    last and up to 12 other sampled rows (rows are independent), and every output of those rows is
+    compared at the north-star tolerance."""
+    rng = np.random.default_rng(seed)
+    device = torch.device("cuda")
+    done = 0
+    while done < count:
+        I = int(rng.integers(1, 41)) if rng.random() < 0.7 else int(rng.integers(41, 1100))
+        u = rng.random()
+        H = int(rng.integers(1, 129)) if u < 0.35 else int(rng.integers(129, 513)) if u < 0.75 else \
+            int(rng.integers(513, 1025))
+        L = int(rng.integers(1, 5))
+        O = 0 if rng.random() < 0.15 else int(rng.integers(1, 40))
+        B = int(rng.integers(1, 1500)) if H <= 128 else int(rng.integers(1, 800))
+        T = int(rng.integers(1, 40)) if rng.random() < 0.7 else int(rng.integers(40, 200))
+        rows = np.unique(np.concatenate([rng.choice(B, min(B, 12), replace=False), [0, B - 1]]))
+        if len(rows) * T * L * 4 * H * (I + H) > 6e8:
+            continue  # keep the oracle to a fraction of a second per case
+        ragged = rng.random() < 0.5
+        with_state = rng.random() < 0.4
+        _say(f"large-batch sweep {done}: I={I} H={H} L={L} O={O} B={B} T={T} ragged={ragged} state={with_state}")
+        torch.manual_seed(int(rng.integers(1 << 30)))
+        lstm = torch.nn.LSTM(I, H, L, batch_first=True)
+        head = torch.nn.Linear(H, O) if O else None
+        x = torch.randn(B, T, I, generator=torch.Generator().manual_seed(done))
+        lengths = torch.tensor(rng.integers(0, T + 1, B), dtype=torch.int64) if ragged else None
+        h0 = (0.5 * torch.randn(L, B, H)).half() if with_state else None
+        c0 = (0.5 * torch.randn(L, B, H)).half() if with_state else None
+        probes = sorted(set(int(p) for p in rng.integers(1, T + 1, 2)))
+        params = [[getattr(lstm, f"{n}_l{l}").detach().cuda() for l in range(L)]
+                  for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+        packed = gpu.pack(*params, head.weight.detach().cuda() if head else None,
+                          head.bias.detach().cuda() if head else None)
+        res = gpu.forward(packed, (I, H, L, O), x.to(device, torch.float16), lengths=lengths,
+                          h0=None if h0 is None else h0.to(device), c0=None if c0 is None else c0.to(device),
+                          want_out=O > 0, want_seq=True, want_state=True, probe_steps=probes, check_status=True)
+        r = torch.from_numpy(rows)
+        want = oracle.lstm_forward(x[r].numpy(), oracle_layers(lstm),
+                                   lengths=None if lengths is None else lengths[r].numpy(),
+                                   h0=None if h0 is None else h0[:, r].float().numpy(),
+                                   c0=None if c0 is None else c0[:, r].float().numpy(),
+                                   probe_steps=probes, want_seq=True)
+        rd = r.to(device)
+        tag = f"large-batch sweep {done}"
+        assert_close(res["out_seq"][rd].float().cpu().numpy(), want["out_seq"], what=f"{tag} out_seq")
+        assert_close(res["h_n"][:, rd].float().cpu().numpy(), want["h_n"], what=f"{tag} h_n")
+        assert_close(res["c_n"][:, rd].float().cpu().numpy(), want["c_n"], what=f"{tag} c_n")
+        assert_close(res["probe_h"][:, :, rd].cpu().numpy(), want["probe_h"], what=f"{tag} probe_h")
+        assert_close(res["probe_c"][:, :, rd].cpu().numpy(), want["probe_c"], what=f"{tag} probe_c")
+        if O:
+            w_head = oracle.linear(want["h_n"][-1], *linear_params(head))
+            assert_close(res["out"][rd].float().cpu().numpy(), w_head, what=f"{tag} head")
+        done += 1

@@ -140,6 +140,8 @@ template <int HP, bool X0>
 __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
   using C = Rec<HP>;
   constexpr int S = C::kS, HS = C::kHs, KCH = C::kKch, NJ = C::kNj, UPW = C::kUpw;
+  // K-chunks by which tile 0's MFMA chain leads tile 1's (NJ = 2; see the step), per padded H.
+  constexpr int kLead = NJ != 2 ? 0 : HP == 512 ? 8 : HP == 256 ? 4 : 0;
   constexpr int NT = 512, FV = 64;
   constexpr int PW = C::kWords / 2;      // packed words of one step's h of a tile (4 fp16 each)
   constexpr int G = (S - 1) * 2 * HS;    // 16-byte loads of the siblings' words per workgroup and step
@@ -397,18 +399,64 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
     // The h fragments are read from LDS four K-chunks ahead of their MFMAs (one read in flight
     // per chunk would leave the matrix core waiting for LDS latency at every chunk).
     constexpr int kAhead = KCH < 4 ? KCH : 4;
-    f16x8 bq[kAhead];
+    float cl0 = 0.f, hl0 = 0.f;  // unit eu's c and h of this step when chain 0 leads (kLead > 0)
+    if constexpr (kLead > 0) {
+      // Chain 0 (unit eu) runs kLead K-chunks ahead of chain 1 (unit eu + 4), and unit eu's cell
+      // update is interleaved with chain 1's last kLead MFMAs instead of waiting for both chains:
+      // the second wave of a SIMD, whose gate math is the step's critical path, starts it ~kLead
+      // MFMAs earlier.  Fragment k is held from chain 0's MFMA to chain 1's.  Each chain sums in
+      // the same order as before, so results are bit-identical (interleaved runs on two boxes: C4
+      // 9.46-9.48 -> 9.38-9.41 ms on one, within its drift on the other; H512 B320 -0.5% to -1.5%;
+      // I300 H256 -4% to -5% at a lead of 4; a lead of 8 at H 256 leaves no MFMA of chain 1 beside
+      // chain 0's and was 1.5% slower there).
+      constexpr int R = kAhead + kLead;
+      f16x8 bq[R];
 #pragma unroll
-    for (int i = 0; i < kAhead; ++i) bq[i] = hprev[i * FV + lane];
+      for (int i = 0; i < kAhead; ++i) bq[i] = hprev[i * FV + lane];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int kc = 0; kc < KCH; ++kc) {
-      const f16x8 bv = bq[kc % kAhead];
-      if (kc + kAhead < KCH) bq[kc % kAhead] = hprev[(kc + kAhead) * FV + lane];
-      if constexpr (NJ == 2) {
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][0], bv, acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][1], bv, acc[1], 0, 0, 0);
-      } else {
-        acc[kc & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][0], bv, acc[kc & 1], 0, 0, 0);
+      for (int p = 0; p < KCH; ++p) {
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[p][0], bq[p % R], acc[0], 0, 0, 0);
+        if (p >= kLead)
+          acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[p - kLead][1], bq[(p - kLead) % R], acc[1], 0, 0, 0);
+        if (p + kAhead < KCH) bq[(p + kAhead) % R] = hprev[(p + kAhead) * FV + lane];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // chain 1's last kLead MFMAs, each followed by a share of unit 0's cell update (~32 VALU
+      // instructions; masks: 0x008 MFMA, 0x002 VALU)
+#pragma unroll
+      for (int p = KCH; p < KCH + kLead; ++p)
+        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[p - kLead][1], bq[(p - kLead) % R], acc[1], 0, 0, 0);
+      {
+        float cn = c[0], hn;
+        lstm_cell(acc[0][0], acc[0][1], acc[0][2], acc[0][3], cn, hn);
+        cl0 = cn;
+        hl0 = hn;
+        asm volatile("" : "+v"(cl0), "+v"(hl0));
+      }
+#pragma unroll
+      for (int p = 0; p < kLead; ++p) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (kLead >= 8)
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        else
+          __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      f16x8 bq[kAhead];
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i) bq[i] = hprev[i * FV + lane];
+#pragma unroll
+      for (int kc = 0; kc < KCH; ++kc) {
+        const f16x8 bv = bq[kc % kAhead];
+        if (kc + kAhead < KCH) bq[kc % kAhead] = hprev[(kc + kAhead) * FV + lane];
+        if constexpr (NJ == 2) {
+          acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][0], bv, acc[0], 0, 0, 0);
+          acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][1], bv, acc[1], 0, 0, 0);
+        } else {
+          acc[kc & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[kc][0], bv, acc[kc & 1], 0, 0, 0);
+        }
       }
     }
     // h_{t-1} of this slice's units, 16 bytes per thread of the first 2 HS threads, stored below as
@@ -427,6 +475,11 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       float cn[NJ], hn[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
+        if (kLead > 0 && j == 0) {
+          cn[0] = cl0;
+          hn[0] = hl0;
+          continue;
+        }
         cn[j] = c[j];
         lstm_cell(z[0][j], z[1][j], z[2][j], z[3][j], cn[j], hn[j]);
       }

@@ -407,8 +407,8 @@ __global__ void __launch_bounds__(512) lstm_rec_kernel(ForwardArgs a) {
       // MFMAs earlier.  Fragment k is held from chain 0's MFMA to chain 1's.  Each chain sums in
       // the same order as before, so results are bit-identical (interleaved runs on two boxes: C4
       // 9.46-9.48 -> 9.38-9.41 ms on one, within its drift on the other; H512 B320 -0.5% to -1.5%;
-      // I300 H256 -4% to -5% at a lead of 4; a lead of 8 at H 256 leaves no MFMA of chain 1 beside
-      // chain 0's and was 1.5% slower there).
+      // I300 H256 -4% to -5% at a lead of 4; at H 256 a lead of 6 was 3.5% and one of 8, which leaves
+      // no MFMA of chain 1 beside chain 0's, 1.5% slower; at H 128 a lead of 2 measured no change).
       constexpr int R = kAhead + kLead;
       f16x8 bq[R];
 #pragma unroll

@@ -208,9 +208,14 @@ proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* 
 //     so their loads read zeros and their stores are dropped (no clamping);
 //   * the W fragments of a k-step are read from LDS two ahead of the MFMAs that use them (3 live
 //     instead of 8), and scheduling groups fix each step's issue order: the ring's 4 loads, 2 W
-//     reads, then 6 x (4 MFMAs, 1 W read) and 8 MFMAs.
+//     reads, then 6 x (4 MFMAs, 1 W read) and 8 MFMAs;
+//   * a tile's result is converted and stored during the next tile's first k-step, each pair of
+//     column blocks right before that step's MFMAs overwrite its accumulators, instead of in an
+//     epilogue during which the wave issues no MFMAs (the first tile stores through a descriptor
+//     of no bytes, the last after the loop).
 // [512000,512]x[512,2048] 1.03-1.05 -> 0.966-0.98 ms, [512000,128]x[128,512] 0.117 -> 0.109 ms
-// (interleaved runs on one box each).
+// (interleaved runs on one box each); the stores in the next tile's first step: 0.943-0.951 ->
+// 0.933-0.935 ms and 0.105-0.106 -> 0.104-0.106 ms, bit-identical.
 template <int KS>
 __global__ void __launch_bounds__(kGemmThreads)
 proj_gemm_blocked_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* __restrict__ W,
@@ -261,71 +266,112 @@ proj_gemm_blocked_kernel(const _Float16* __restrict__ X, long long ldx, const _F
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  for (;;) {
-    const int nmt = mt + m_groups;
-    const int pmt = nmt < tiles_m ? nmt : mt;  // prefetch target past the last tile: reload this one
-    const auto rc = xrs(mt), rn = xrs(pmt);
-    f32x4 acc[kGemmWM][8];
+  f32x4 acc[kGemmWM][8];
+  // k-step s of the tile whose X rows rc describes (rn: the next tile's, for the ring's loads past
+  // this tile's last step).  Step 0 starts every accumulator from zero; with `out` (a fused step 0)
+  // each accumulator pair of the previous tile is converted and stored right before the step's
+  // MFMAs overwrite it, so the epilogue's VALU work and stores run beside the next tile's first
+  // MFMAs instead of stalling the matrix core.
+  auto kstep = [&](int s, __amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rn, const __amdgpu_buffer_rsrc_t* out)
+      __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      const int sn = s + kRing - 1;  // this tile's step sn, or the next tile's first steps
+      if (sn < KS)
+        ld(rc, sn, xr[sn % kRing]);
+      else
+        ld(rn, sn - KS, xr[sn % kRing]);
+    }
+    f16x8 wa[3];
+    wa[0] = wl[(s * 8 + 0) * 64 + lane];
+    wa[1] = wl[(s * 8 + 1) * 64 + lane];
 #pragma unroll
-    for (int a = 0; a < kGemmWM; ++a)
+    for (int b = 0; b < 8; ++b) {
+      if (b + 2 < 8) wa[(b + 2) % 3] = wl[(s * 8 + b + 2) * 64 + lane];
+      if (out && b % 2 == 0) {
+        // the previous tile's column blocks n0 / 32 + b / 2: blocks 32 mt + 4 wave + a
 #pragma unroll
-      for (int b = 0; b < 8; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int a = 0; a < kGemmWM; ++a) {
+          f16x8 v;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      __builtin_amdgcn_sched_barrier(0);
-      {
-        const int sn = s + kRing - 1;  // this tile's step sn, or the next tile's first steps
-        if (sn < KS)
-          ld(rc, sn, xr[sn % kRing]);
-        else
-          ld(rn, sn - KS, xr[sn % kRing]);
+          for (int j = 0; j < 4; ++j) {
+            v[j] = (_Float16)acc[a][b][j];
+            v[4 + j] = (_Float16)acc[a][b + 1][j];
+          }
+          // nontemporal (cache policy 2), as in proj_gemm_kernel
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v),
+                                                 *out, voff, a * ca + (b / 2) * 1024, 2);
+        }
       }
-      f16x8 wa[3];
-      wa[0] = wl[(s * 8 + 0) * 64 + lane];
-      wa[1] = wl[(s * 8 + 1) * 64 + lane];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        if (b + 2 < 8) wa[(b + 2) % 3] = wl[(s * 8 + b + 2) * 64 + lane];
-#pragma unroll
-        for (int a = 0; a < kGemmWM; ++a)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[b % 3], xr[s % kRing][a], acc[a][b], 0, 0, 0);
-      }
-      // issue order (masks: 0x020 vector-memory reads, 0x100 LDS reads, 0x008 MFMA)
-      __builtin_amdgcn_sched_group_barrier(0x020, kGemmWM, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      for (int a = 0; a < kGemmWM; ++a)
+        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[b % 3], xr[s % kRing][a],
+                                                          s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[a][b], 0, 0, 0);
+    }
+    // issue order (masks: 0x020 vector-memory reads, 0x100 LDS reads, 0x008 MFMA, 0x002 VALU,
+    // 0x040 vector-memory writes)
+    __builtin_amdgcn_sched_group_barrier(0x020, kGemmWM, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    if (!out) {
 #pragma unroll
       for (int g = 0; g < 6; ++g) {
         __builtin_amdgcn_sched_group_barrier(0x008, kGemmWM, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 2 * kGemmWM, 0);
+    } else {
+      // per pair of column blocks: the conversions and stores of the previous tile's pair, then
+      // the MFMAs that overwrite it (each with the W read two blocks ahead)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x002, 4 * kGemmWM, 0);
+        __builtin_amdgcn_sched_group_barrier(0x040, kGemmWM, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kGemmWM, 0);
+        if (g < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kGemmWM, 0);
+        if (g < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
     }
+  };
+  // the result descriptor of tile t: blocks 32 t + 4 wave + a, column blocks n0 / 32 + p; rows at or
+  // past M fall outside it
+  auto crs = [&](int t) {
+    const int mb = t * (kGemmBM / 16) + wave * kGemmWM;
+    const int rem = max(min(max(nblk - mb, 0), max_cb) * ca - n0 * 32, 0);
+    return __builtin_amdgcn_make_buffer_rsrc(C + (mb < nblk ? (size_t)mb * ldc * 16 + (size_t)n0 * 16 : 0), 0, rem,
+                                             0x00020000);
+  };
+  // The previous tile's result descriptor: none before the first tile (its stores are dropped).
+  __amdgpu_buffer_rsrc_t prev = __builtin_amdgcn_make_buffer_rsrc(C, 0, 0, 0x00020000);
+#pragma unroll
+  for (int a = 0; a < kGemmWM; ++a)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (;;) {
+    const int nmt = mt + m_groups;
+    const int pmt = nmt < tiles_m ? nmt : mt;  // prefetch target past the last tile: reload this one
+    const auto rc = xrs(mt), rn = xrs(pmt);
+    kstep(0, rc, rn, &prev);
+#pragma unroll
+    for (int s = 1; s < KS; ++s) kstep(s, rc, rn, nullptr);
     __builtin_amdgcn_sched_barrier(0);
-    {
-      // the tile's result: blocks 32 mt + 4 wave + a, column blocks n0 / 32 + p; rows at or past M
-      // fall outside the descriptor
-      const int mb = mt * (kGemmBM / 16) + wave * kGemmWM;
-      const int rem = max(min(max(nblk - mb, 0), max_cb) * ca - n0 * 32, 0);
-      const auto rs = __builtin_amdgcn_make_buffer_rsrc(C + (mb < nblk ? (size_t)mb * ldc * 16 + (size_t)n0 * 16 : 0), 0,
-                                                        rem, 0x00020000);
-#pragma unroll
-      for (int a = 0; a < kGemmWM; ++a)
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          f16x8 v;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            v[j] = (_Float16)acc[a][2 * p][j];
-            v[4 + j] = (_Float16)acc[a][2 * p + 1][j];
-          }
-          // nontemporal (cache policy 2), as in proj_gemm_kernel
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v),
-                                                 rs, voff, a * ca + p * 1024, 2);
-        }
-    }
+    prev = crs(mt);
     if (nmt >= tiles_m) break;
     mt = nmt;
   }
+#pragma unroll
+  for (int a = 0; a < kGemmWM; ++a)
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      f16x8 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = (_Float16)acc[a][2 * p][j];
+        v[4 + j] = (_Float16)acc[a][2 * p + 1][j];
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v),
+                                             prev, voff, a * ca + p * 1024, 2);
+    }
 }
 
 }  // namespace

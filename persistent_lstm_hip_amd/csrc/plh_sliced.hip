@@ -66,6 +66,7 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   __shared__ int s_fail;
   __shared__ int s_tlen;
   __shared__ int s_l2;
+  __shared__ uint32_t s_up[NTI];  // upstream counter of tile i as last read by wave 0
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -86,6 +87,10 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   if (threadIdx.x == 0) {
     s_tlen = 0;
     s_fail = 0;
+    // Zeroed before the first barrier: every staging wave reads it in the prologue, and LDS keeps
+    // what an earlier workgroup left there (a stale upstream count would let a wave load hand-off
+    // steps that are not yet published).
+    for (int i = 0; i < NTI; ++i) s_up[i] = 0;
     // With xcd_map the S slices of a (layer, tile group) are dispatched to one XCD; checked here,
     // and only then do they exchange h through that XCD's L2 (same_xcd_group; the table of the
     // groups' XCD ids follows the rings).
@@ -229,7 +234,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
   constexpr int CS = kSlicedCounterStride;
   auto up_ctr = [&](int i) -> uint32_t* { return a.counters + ((size_t)(layer - 1) * a.ntile + tile0 + i) * CS; };
   auto my_ctr = [&](int i) -> uint32_t* { return a.counters + ((size_t)layer * a.ntile + tile0 + i) * CS; };
-  __shared__ uint32_t s_up[NTI];  // upstream counter of tile i as last read by wave 0
   int pub[NTI];                   // groups of tile i published (thread 0)
   int avail[NTI];                 // groups of tile i known published upstream (this wave)
   uint32_t cup[NTI];              // wave 0: upstream counter of tile i, loaded a step earlier
@@ -238,7 +242,6 @@ __global__ void __launch_bounds__(512) lstm_sliced_kernel(ForwardArgs a) {
     pub[i] = 0;
     avail[i] = 0;
     cup[i] = 0;
-    if (threadIdx.x == 0) s_up[i] = 0;
   }
   auto load_counter = [&](int i) {
     if (has_up && wave == 0) cup[i] = __hip_atomic_load(up_ctr(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -970,3 +970,45 @@ def test_random_large_batch_sweep(gpu, seed, count):
             w_head = oracle.linear(want["h_n"][-1], *linear_params(head))
             assert_close(res["out"][rd].float().cpu().numpy(), w_head, what=f"{tag} head")
         done += 1
+
+
+def test_sliced_two_tile_handoff_repeated(gpu):
+    """Regression: the sliced kernel's staging waves read the shared copy of the upstream hand-off
+    count in their first input wait.  It was zeroed only after the kernel's first barrier, so a wave
+    could read what an earlier workgroup had left in LDS, take unpublished steps of the previous
+    layer's hand-off as published and compute a whole 16-row tile from them (about 0.5% of forwards
+    at padded H 256 with two tiles per workgroup, seen in random sweeps).  Two such geometries,
+    alternated 200 times each: every forward equals its geometry's first bitwise, and each first
+    forward matches the oracle on sampled rows."""
+    device = torch.device("cuda")
+    cases = []
+    for I, H, L, O, B, T in ((20, 200, 3, 5, 600, 12), (7, 230, 4, 0, 300, 9)):
+        torch.manual_seed(7 * H + B)
+        lstm = torch.nn.LSTM(I, H, L, batch_first=True)
+        head = torch.nn.Linear(H, O) if O else None
+        x = torch.randn(B, T, I, generator=torch.Generator().manual_seed(B))
+        params = [[getattr(lstm, f"{n}_l{l}").detach().cuda() for l in range(L)]
+                  for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+        packed = gpu.pack(*params, head.weight.detach().cuda() if head else None,
+                          head.bias.detach().cuda() if head else None)
+        cases.append(((I, H, L, O), lstm, x, x.to(device, torch.float16), packed))
+
+    def run(c):
+        dims, _, _, xd, packed = c
+        return gpu.forward(packed, dims, xd, want_out=dims[3] > 0, want_seq=True, want_state=True,
+                           check_status=True)["out_seq"]
+
+    firsts = [run(c).clone() for c in cases]
+    for c, first in zip(cases, firsts):
+        dims, lstm, x, _, _ = c
+        rows = np.unique(np.r_[0:4, np.linspace(4, x.shape[0] - 1, 28).astype(int)])
+        want = oracle.lstm_forward(x.numpy()[rows], oracle_layers(lstm), want_seq=True)["out_seq"]
+        assert_close(first[torch.from_numpy(rows).to(device)].float().cpu().numpy(), want,
+                     what=f"H={dims[1]} first forward vs oracle")
+    _say("sliced two-tile hand-off: 400 alternating forwards")
+    bad = []
+    for it in range(200):
+        for k, c in enumerate(cases):
+            if not torch.equal(run(c), firsts[k]):
+                bad.append((it, k))
+    assert not bad, f"{len(bad)} forwards differ from their geometry's first: {bad[:10]}"

@@ -197,7 +197,7 @@ proj_gemm_kernel(const _Float16* __restrict__ X, long long ldx, const _Float16* 
   }
 }
 
-// The blocked layouts at K = 32 KS (KS = 4, 8 or 16: K = 128, 256, 512), with the k-steps of an m-tile
+// The blocked layouts at K = 32 KS (KS = 4, 8, 12 or 16: K = 128, 256, 384, 512), with the k-steps of an m-tile
 // unrolled at compile time.  The same work split, W slice and X ring as proj_gemm_kernel, written so
 // that the compiler keeps the ring's loads kRing - 1 steps ahead everywhere: with a runtime k-loop the
 // register allocator rotated the ring slots through the accumulators and waited for every
@@ -391,10 +391,11 @@ hipError_t launch_proj_gemm(const _Float16* X, long long ldx, const _Float16* W,
   // m-tile), placed so that an m-group's slices share an XCD.
   const int m_groups = std::max(1, std::min(tiles_m, std::max(cus, 1) / n_slices));
   const int grid = ((m_groups + 7) / 8) * 8 * n_slices;
-  // The compile-time-K kernel where one is built (at K = 384 it spills, and the generic kernel runs).
+  // The compile-time-K kernel where one is built (other K: the generic kernel).
   auto* fk = !blocked || ldc > (1 << 20) ? nullptr
              : K == 128                   ? proj_gemm_blocked_kernel<4>
              : K == 256                   ? proj_gemm_blocked_kernel<8>
+             : K == 384                   ? proj_gemm_blocked_kernel<12>
              : K == 512                   ? proj_gemm_blocked_kernel<16>
                                           : nullptr;
   if (fk) {

@@ -517,18 +517,19 @@ lstm_wavefront_kernel(ForwardArgs a) {
 
 }  // namespace
 
-// Steps per hand-off chunk (compile-time tuning knob).
-#ifndef PLH_CHUNK_STEPS
-#define PLH_CHUNK_STEPS 8
-#endif
-constexpr int kChunk = PLH_CHUNK_STEPS;
+// Steps per hand-off chunk: 16 with 8-row tiles at padded H <= 64, where a step is short and the
+// per-chunk work weighs more than the longer lag between layers (H64 L2 B512 -5.4%, H32 L8 -3.9%;
+// at H 128 it was slower, C2 +0.9%, C5 +1.3%, and with 16-row tiles it does not fit the LDS);
+// 8 otherwise.
+template <int HP, int ROWS>
+constexpr int chunk_steps() { return ROWS == 8 && HP <= 64 ? 16 : 8; }
 
 template <int ROWS, bool RAGGED>
 static const void* wavefront_kernel_rows(int HP) {
   switch (HP) {
-    case 32: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<32, ROWS, kChunk, RAGGED>);
-    case 64: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<64, ROWS, kChunk, RAGGED>);
-    case 128: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<128, ROWS, kChunk, RAGGED>);
+    case 32: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<32, ROWS, chunk_steps<32, ROWS>(), RAGGED>);
+    case 64: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<64, ROWS, chunk_steps<64, ROWS>(), RAGGED>);
+    case 128: return reinterpret_cast<const void*>(&lstm_wavefront_kernel<128, ROWS, chunk_steps<128, ROWS>(), RAGGED>);
     default: return nullptr;
   }
 }
